@@ -1,0 +1,71 @@
+"""Compile the HIP sources under fgw_amd/csrc into fgw_amd/libfgw_mha.so for gfx950.
+
+Every call rebuilds from scratch (objects under fgw_amd/_build). Run directly
+(`python -m fgw_amd.build`) or through __graft_entry__.build().
+"""
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import pathlib
+import shutil
+import subprocess
+import sys
+
+PACKAGE = pathlib.Path(__file__).resolve().parent
+CSRC = PACKAGE / "csrc"
+BUILD = PACKAGE / "_build"
+LIBRARY = PACKAGE / "libfgw_mha.so"
+ARCH = "gfx950"
+
+# Packed FP32 instructions stay disabled in all device code.
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def hipcc() -> str:
+    path = os.environ.get("HIPCC") or shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not pathlib.Path(path).exists():
+        raise RuntimeError(f"hipcc not found (looked for {path})")
+    return path
+
+
+def _compile(source: pathlib.Path) -> pathlib.Path:
+    obj = BUILD / (source.stem + ".o")
+    cmd = [hipcc(), *HIP_FLAGS, "-c", str(source), "-o", str(obj)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "'-packed-fp32-ops' is not a recognized feature"
+    log = "\n".join(line for line in (proc.stdout + proc.stderr).splitlines() if noise not in line)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {source.name}:\n{log}")
+    if log.strip():
+        print(log, file=sys.stderr)
+    return obj
+
+
+def build(jobs: int | None = None, verbose: bool = True) -> pathlib.Path:
+    """Compile all csrc/*.hip and link the shared library; returns its path."""
+    sources = sorted(CSRC.glob("*.hip"))
+    if not sources:
+        raise RuntimeError(f"no HIP sources under {CSRC}")
+    if BUILD.exists():
+        shutil.rmtree(BUILD)
+    BUILD.mkdir(parents=True)
+    jobs = jobs or min(len(sources), max(1, min(16, os.cpu_count() or 1)))
+    with cf.ThreadPoolExecutor(max_workers=jobs) as pool:
+        objects = list(pool.map(_compile, sources))
+    tmp = LIBRARY.with_suffix(".so.tmp")
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-o", str(tmp), *map(str, objects)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"link failed:\n{proc.stdout}{proc.stderr}")
+    os.replace(tmp, LIBRARY)
+    if verbose:
+        print(f"built {LIBRARY} from {len(sources)} sources", file=sys.stderr)
+    return LIBRARY
+
+
+if __name__ == "__main__":
+    build()

@@ -1,0 +1,348 @@
+// C ABI of the paged MHA operator: validation, planning and dispatch.
+// Declarations and reference citations: include/fgw_mha.h.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+
+#include "../../include/fgw_mha.h"
+#include "fmha_aux.h"
+#include "fmha_kernel.h"
+#include "fmha_registry.h"
+
+namespace fgw_mha {
+
+FGW_MHA_FOR_DPAD_LO(FGW_MHA_EXTERN, true)
+FGW_MHA_FOR_DPAD_HI(FGW_MHA_EXTERN, true)
+FGW_MHA_FOR_DPAD_LO(FGW_MHA_EXTERN, false)
+FGW_MHA_FOR_DPAD_HI(FGW_MHA_EXTERN, false)
+
+#define FGW_ENTRY(BF, DP, LY) \
+  if (bf16 == BF && dpad == DP && layout == LY) return FwdEntry{&launch_fwd<BF, DP, LY>, &occupancy_fwd<BF, DP, LY>};
+#define FGW_ENTRIES(BF, DP) FGW_ENTRY(BF, DP, kLayoutQuery) FGW_ENTRY(BF, DP, kLayoutKey)
+
+FwdEntry fwd_entry(bool bf16, int dpad, int layout) {
+  FGW_MHA_FOR_DPAD_LO(FGW_ENTRIES, true)
+  FGW_MHA_FOR_DPAD_HI(FGW_ENTRIES, true)
+  FGW_MHA_FOR_DPAD_LO(FGW_ENTRIES, false)
+  FGW_MHA_FOR_DPAD_HI(FGW_ENTRIES, false)
+  return FwdEntry{nullptr, nullptr};
+}
+
+hipError_t launch_merge(bool bf16, const MergeParams& p, hipStream_t stream) {
+  const int64_t rows = (int64_t)p.batch * p.sq * p.heads;
+  const dim3 grid((unsigned)((rows + 3) / 4));
+  if (bf16) {
+    merge_kernel<true><<<grid, dim3(256), 0, stream>>>(p);
+  } else {
+    merge_kernel<false><<<grid, dim3(256), 0, stream>>>(p);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_gather(const GatherParams& p, hipStream_t stream) {
+  const int64_t rows = (int64_t)p.batch * p.out_len;
+  gather_kernel<<<dim3((unsigned)rows), dim3(256), 0, stream>>>(p);
+  return hipGetLastError();
+}
+
+}  // namespace fgw_mha
+
+using namespace fgw_mha;
+
+namespace {
+
+thread_local char g_error[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_error, sizeof(g_error), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(FGW_MHA_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+constexpr int kMaxSplits = 128;
+constexpr int kAutoMaxSplits = 64;
+constexpr int kMinRoundsPerSplit = 2;
+
+// Keys one program consumes per loop round, per layout.
+int keys_per_round(int layout) { return layout == kLayoutQuery ? 64 : 4 * 32; }
+int rows_per_tile(int layout) { return layout == kLayoutQuery ? 128 : 32; }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Granlund-Montgomery constants for the division of positions by page_size.
+void page_divisor(uint32_t page, uint32_t* magic, uint32_t* shift) {
+  if (page <= 1) {
+    *magic = 0;
+    *shift = 0;
+    return;
+  }
+  uint32_t l = 0;
+  while ((1ull << l) < page) ++l;
+  const uint64_t m = (((1ull << 32) * ((1ull << l) - page)) / page) + 1;
+  *magic = (uint32_t)m;
+  *shift = l;
+}
+
+int check_shape(const fgw_mha_shape* s) {
+  if (!s) return fail(FGW_MHA_EINVAL, "shape is NULL");
+  if (s->batch <= 0 || s->sq <= 0 || s->heads <= 0 || s->dim <= 0)
+    return fail(FGW_MHA_EINVAL, "positive Q extents and rank-2 table required");
+  if (s->page_size <= 0 || s->pool_rows <= 0 || s->pool_rows % s->page_size || s->width <= 0)
+    return fail(FGW_MHA_EINVAL,
+                "positive page size, whole pool pages and positive table width required");
+  if (s->dtype != FGW_MHA_FLOAT16 && s->dtype != FGW_MHA_BFLOAT16)
+    return fail(FGW_MHA_EINVAL, "matching FP16/BF16 Q/K/V required");
+  if (s->dim < 16 || s->dim > 256 || s->dim % 16)
+    return fail(FGW_MHA_EUNSUPPORTED, "D must be in [16, 256] and divisible by 16");
+  if ((int64_t)s->width * s->page_size > INT32_MAX)
+    return fail(FGW_MHA_EUNSUPPORTED, "table capacity exceeds 2^31 tokens");
+  if ((int64_t)s->batch * s->sq * s->heads > INT32_MAX)
+    return fail(FGW_MHA_EUNSUPPORTED, "B*Sq*H exceeds 2^31 rows");
+  return FGW_MHA_OK;
+}
+
+int check_plan(const fgw_mha_shape* s, const fgw_mha_plan_t* p) {
+  if (!p) return fail(FGW_MHA_EINVAL, "plan is NULL");
+  if (p->layout != kLayoutQuery && p->layout != kLayoutKey)
+    return fail(FGW_MHA_EINVAL, "plan layout %d is not a kernel layout", p->layout);
+  const int rows = rows_per_tile(p->layout);
+  const int q_tiles = (s->sq + rows - 1) / rows;
+  const int64_t tasks = (int64_t)s->batch * s->heads * q_tiles;
+  if (p->rows_per_tile != rows || p->q_tiles != q_tiles || p->query_tile_tasks != tasks ||
+      p->num_splits < 1 || p->num_splits > kMaxSplits ||
+      p->work_items != tasks * p->num_splits || p->grid < 1 || p->grid > p->work_items ||
+      p->dim_padded != dim_tile(s->dim) || p->execution_mode != (p->num_splits > 1 ? 1 : 0))
+    return fail(FGW_MHA_EINVAL, "plan does not match the shape; call fgw_mha_plan");
+  return FGW_MHA_OK;
+}
+
+int check_tensors(const fgw_mha_tensors* t, bool need_inputs, bool need_out, bool need_ws) {
+  if (!t) return fail(FGW_MHA_EINVAL, "tensors is NULL");
+  if (need_inputs) {
+    if (!t->q || !t->k_cache || !t->v_cache || !t->block_table || !t->cache_seqlens)
+      return fail(FGW_MHA_EINVAL, "input pointer is NULL");
+    if (!aligned16(t->q) || !aligned16(t->k_cache) || !aligned16(t->v_cache))
+      return fail(FGW_MHA_EINVAL, "Q/K/V must be 16-byte aligned");
+  }
+  if (need_out && (!t->out || !aligned16(t->out)))
+    return fail(FGW_MHA_EINVAL, "output must be a 16-byte aligned buffer");
+  if (need_ws && (!t->parts || !t->lse || !aligned16(t->parts)))
+    return fail(FGW_MHA_EINVAL, "split workspace (parts, lse) required, parts 16-byte aligned");
+  return FGW_MHA_OK;
+}
+
+FwdParams make_params(const fgw_mha_shape* s, const fgw_mha_plan_t* p, const fgw_mha_tensors* t,
+                      int mode) {
+  FwdParams f;
+  f.q = t->q;
+  f.k = t->k_cache;
+  f.v = t->v_cache;
+  f.table = t->block_table;
+  f.lengths = t->cache_seqlens;
+  f.out = t->out;
+  f.parts = t->parts;
+  f.lse = t->lse;
+  f.pool_rows = s->pool_rows;
+  f.batch = s->batch;
+  f.sq = s->sq;
+  f.heads = s->heads;
+  f.dim = s->dim;
+  f.width = s->width;
+  f.page_size = s->page_size;
+  f.causal = s->causal ? 1 : 0;
+  f.splits = p->num_splits;
+  f.q_tiles = p->q_tiles;
+  f.work = p->work_items;
+  f.mode = mode;
+  page_divisor((uint32_t)s->page_size, &f.page_magic, &f.page_shift);
+  f.scale_log2 = (float)(1.4426950408889634 / __builtin_sqrt((double)s->dim));
+  return f;
+}
+
+int launch_partial_kernel(const fgw_mha_shape* s, const fgw_mha_plan_t* p,
+                          const fgw_mha_tensors* t, int mode, hipStream_t stream) {
+  const FwdEntry e = fwd_entry(s->dtype == FGW_MHA_BFLOAT16, p->dim_padded, p->layout);
+  if (!e.launch) return fail(FGW_MHA_EUNSUPPORTED, "no kernel for dim tile %d", p->dim_padded);
+  const FwdParams f = make_params(s, p, t, mode);
+  const hipError_t err = e.launch(f, p->grid, stream);
+  return err == hipSuccess ? FGW_MHA_OK : hip_fail(err, "forward kernel launch");
+}
+
+int launch_merge_kernel(const fgw_mha_shape* s, const fgw_mha_plan_t* p, const fgw_mha_tensors* t,
+                        hipStream_t stream) {
+  MergeParams m;
+  m.parts = t->parts;
+  m.lse = t->lse;
+  m.out = t->out;
+  m.batch = s->batch;
+  m.sq = s->sq;
+  m.heads = s->heads;
+  m.dim = s->dim;
+  m.splits = p->num_splits;
+  const hipError_t err = launch_merge(s->dtype == FGW_MHA_BFLOAT16, m, stream);
+  return err == hipSuccess ? FGW_MHA_OK : hip_fail(err, "merge kernel launch");
+}
+
+}  // namespace
+
+extern "C" {
+
+int fgw_mha_abi_version(void) { return FGW_MHA_ABI_VERSION; }
+
+const char* fgw_mha_last_error(void) { return g_error; }
+
+int fgw_mha_query_device(int device, fgw_mha_device_info* info) {
+  if (!info) return fail(FGW_MHA_EINVAL, "info is NULL");
+  hipDeviceProp_t prop;
+  hipError_t err = hipGetDeviceProperties(&prop, device);
+  if (err != hipSuccess) return hip_fail(err, "hipGetDeviceProperties");
+  int current = 0;
+  err = hipGetDevice(&current);
+  if (err != hipSuccess) return hip_fail(err, "hipGetDevice");
+  if (current != device && (err = hipSetDevice(device)) != hipSuccess)
+    return hip_fail(err, "hipSetDevice");
+  info->num_cus = prop.multiProcessorCount;
+  info->arch_gfx950 = std::strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : 0;
+  for (int layout = 0; layout < 2; ++layout) {
+    const int n = fwd_entry(true, 128, layout).occupancy();
+    info->wg_per_cu[layout] = n > 0 ? n : 1;
+  }
+  if (current != device) (void)hipSetDevice(current);
+  return FGW_MHA_OK;
+}
+
+int fgw_mha_plan(const fgw_mha_shape* s, const fgw_mha_request* req,
+                 const fgw_mha_device_info* dev, fgw_mha_plan_t* out) {
+  int rc = check_shape(s);
+  if (rc) return rc;
+  if (!req || !dev || !out) return fail(FGW_MHA_EINVAL, "request/device/plan is NULL");
+  if (dev->num_cus <= 0) return fail(FGW_MHA_EINVAL, "device info has no compute units");
+  int layout = req->layout;
+  if (layout == FGW_MHA_LAYOUT_AUTO) layout = s->sq <= 32 ? kLayoutKey : kLayoutQuery;
+  if (layout != kLayoutQuery && layout != kLayoutKey)
+    return fail(FGW_MHA_EINVAL, "layout must be -1 (auto), 0 (query) or 1 (key)");
+  const int rows = rows_per_tile(layout);
+  const int q_tiles = (s->sq + rows - 1) / rows;
+  const int64_t tasks = (int64_t)s->batch * s->heads * q_tiles;
+  const int64_t capacity = (int64_t)s->width * s->page_size;
+  // KV tiles of 32 tokens, as the reference general route counts them
+  // (cube_general.py:36); more splits than blocks leave empty splits.
+  const int64_t kv_blocks = (capacity + 31) / 32;
+
+  int splits = req->num_splits;
+  if (splits != 0) {
+    if (splits < 1 || splits > kMaxSplits || (splits & (splits - 1)))
+      return fail(FGW_MHA_EINVAL, "num_splits supports None (automatic) or 1/2/4/.../%d",
+                  kMaxSplits);
+    if (splits > kv_blocks)
+      return fail(FGW_MHA_EINVAL,
+                  "num_splits must not exceed the number of KV tiles in table capacity");
+  } else {
+    const int wg = dev->wg_per_cu[layout] > 0 ? dev->wg_per_cu[layout] : 1;
+    const int64_t slots = (int64_t)dev->num_cus * wg;
+    const int64_t min_keys = (int64_t)keys_per_round(layout) * kMinRoundsPerSplit;
+    splits = 1;
+    while (splits < kAutoMaxSplits && tasks * splits < slots &&
+           (int64_t)(splits * 2) * min_keys <= capacity)
+      splits *= 2;
+  }
+  const int64_t work = tasks * splits;
+  if (work > INT32_MAX) return fail(FGW_MHA_EUNSUPPORTED, "work items exceed 2^31");
+
+  int64_t grid = work;
+  if (req->persistent_programs < -1)
+    return fail(FGW_MHA_EINVAL, "persistent_programs must be -1, 0 or positive");
+  if (req->persistent_programs == -1) {
+    const int wg = dev->wg_per_cu[layout] > 0 ? dev->wg_per_cu[layout] : 1;
+    const int64_t cap = (int64_t)dev->num_cus * wg;
+    grid = work < cap ? work : cap;
+  } else if (req->persistent_programs > 0) {
+    grid = work < req->persistent_programs ? work : req->persistent_programs;
+  }
+
+  out->layout = layout;
+  out->rows_per_tile = rows;
+  out->q_tiles = q_tiles;
+  out->num_splits = splits;
+  out->query_tile_tasks = (int32_t)tasks;
+  out->work_items = (int32_t)work;
+  out->grid = (int32_t)grid;
+  out->threads = 256;
+  out->execution_mode = splits > 1 ? 1 : 0;
+  out->dim_padded = dim_tile(s->dim);
+  out->parts_floats = splits > 1 ? (int64_t)s->batch * s->heads * splits * s->sq * s->dim : 0;
+  out->lse_floats = splits > 1 ? (int64_t)s->batch * s->heads * splits * s->sq : 0;
+  return FGW_MHA_OK;
+}
+
+int fgw_mha_fwd(const fgw_mha_shape* s, const fgw_mha_plan_t* p, const fgw_mha_tensors* t,
+                hipStream_t stream) {
+  int rc = check_shape(s);
+  if (!rc) rc = check_plan(s, p);
+  if (!rc) rc = check_tensors(t, true, true, p->num_splits > 1);
+  if (rc) return rc;
+  if (p->num_splits == 1) return launch_partial_kernel(s, p, t, 0, stream);
+  rc = launch_partial_kernel(s, p, t, 1, stream);
+  if (rc) return rc;
+  return launch_merge_kernel(s, p, t, stream);
+}
+
+int fgw_mha_partial(const fgw_mha_shape* s, const fgw_mha_plan_t* p, const fgw_mha_tensors* t,
+                    hipStream_t stream) {
+  int rc = check_shape(s);
+  if (!rc) rc = check_plan(s, p);
+  if (!rc) rc = check_tensors(t, true, false, true);
+  if (rc) return rc;
+  return launch_partial_kernel(s, p, t, 1, stream);
+}
+
+int fgw_mha_merge(const fgw_mha_shape* s, const fgw_mha_plan_t* p, const fgw_mha_tensors* t,
+                  hipStream_t stream) {
+  int rc = check_shape(s);
+  if (!rc) rc = check_plan(s, p);
+  if (!rc) rc = check_tensors(t, false, true, true);
+  if (rc) return rc;
+  return launch_merge_kernel(s, p, t, stream);
+}
+
+int fgw_mha_gather_kv(const fgw_mha_shape* s, const fgw_mha_tensors* t, void* out_k, void* out_v,
+                      int32_t out_len, hipStream_t stream) {
+  int rc = check_shape(s);
+  if (rc) return rc;
+  if (!t || !t->k_cache || !t->v_cache || !t->block_table || !t->cache_seqlens || !out_k ||
+      !out_v)
+    return fail(FGW_MHA_EINVAL, "gather needs K/V, table, lengths and two outputs");
+  if (!aligned16(t->k_cache) || !aligned16(t->v_cache) || !aligned16(out_k) || !aligned16(out_v))
+    return fail(FGW_MHA_EINVAL, "gather buffers must be 16-byte aligned");
+  if (out_len <= 0) return fail(FGW_MHA_EINVAL, "out_len must be positive");
+  if ((int64_t)s->batch * out_len > INT32_MAX)
+    return fail(FGW_MHA_EUNSUPPORTED, "B*out_len exceeds 2^31 rows");
+  GatherParams g;
+  g.k = t->k_cache;
+  g.v = t->v_cache;
+  g.table = t->block_table;
+  g.lengths = t->cache_seqlens;
+  g.out_k = out_k;
+  g.out_v = out_v;
+  g.pool_rows = s->pool_rows;
+  g.batch = s->batch;
+  g.heads = s->heads;
+  g.dim = s->dim;
+  g.width = s->width;
+  g.page_size = s->page_size;
+  g.out_len = out_len;
+  page_divisor((uint32_t)s->page_size, &g.page_magic, &g.page_shift);
+  const hipError_t err = launch_gather(g, stream);
+  return err == hipSuccess ? FGW_MHA_OK : hip_fail(err, "gather kernel launch");
+}
+
+}  // extern "C"

@@ -1,0 +1,38 @@
+// Host-side table of the compiled kernel instantiations.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include "fmha_params.h"
+
+namespace fgw_mha {
+
+typedef hipError_t (*FwdLaunchFn)(const FwdParams&, int, hipStream_t);
+typedef int (*OccupancyFn)();
+
+struct FwdEntry {
+  FwdLaunchFn launch;
+  OccupancyFn occupancy;
+};
+
+// Head-dim tiles with a compiled kernel: 32, 64, ..., 256.
+inline int dim_tile(int dim) { return (dim + 31) / 32 * 32; }
+
+FwdEntry fwd_entry(bool bf16, int dpad, int layout);
+hipError_t launch_merge(bool bf16, const MergeParams& p, hipStream_t stream);
+hipError_t launch_gather(const GatherParams& p, hipStream_t stream);
+
+}  // namespace fgw_mha
+
+// Explicit instantiation lists, expanded once per translation unit.
+#define FGW_MHA_FOR_DPAD_LO(X, BF) X(BF, 32) X(BF, 64) X(BF, 96) X(BF, 128)
+#define FGW_MHA_FOR_DPAD_HI(X, BF) X(BF, 160) X(BF, 192) X(BF, 224) X(BF, 256)
+#define FGW_MHA_INSTANTIATE(BF, DP)                                                         \
+  template hipError_t launch_fwd<BF, DP, kLayoutQuery>(const FwdParams&, int, hipStream_t); \
+  template hipError_t launch_fwd<BF, DP, kLayoutKey>(const FwdParams&, int, hipStream_t);   \
+  template int occupancy_fwd<BF, DP, kLayoutQuery>();                                       \
+  template int occupancy_fwd<BF, DP, kLayoutKey>();
+#define FGW_MHA_EXTERN(BF, DP)                                                                     \
+  extern template hipError_t launch_fwd<BF, DP, kLayoutQuery>(const FwdParams&, int, hipStream_t); \
+  extern template hipError_t launch_fwd<BF, DP, kLayoutKey>(const FwdParams&, int, hipStream_t);   \
+  extern template int occupancy_fwd<BF, DP, kLayoutQuery>();                                       \
+  extern template int occupancy_fwd<BF, DP, kLayoutKey>();

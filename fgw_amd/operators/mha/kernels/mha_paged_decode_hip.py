@@ -1,0 +1,269 @@
+"""Paged multi-head attention on MI355X: the operators/mha public entry.
+
+Same public contract as the reference operator
+(operators/mha/kernels/mha_paged_decode_ascend_v7.py:516-570, original
+contract mha_paged_decode_ascend_v0.py:98-126):
+
+  Q [B, Sq, H, D], K/V pool [N, H, D], block table [B, W] int32,
+  cache lengths [B] int32, page_size -> O [B, Sq, H, D] in Q's dtype.
+
+One route serves every supported shape: FP16/BF16, D 16..256 in steps of 16,
+any positive page size with whole pool pages, ragged and empty caches,
+non-causal and right-aligned causal attention, Q from 1 upwards. The work is
+done by hand-written CDNA4 kernels in libfgw_mha.so (fgw_amd/csrc), reached
+through its C ABI; there is no other implementation to fall back to.
+
+build_kernel returns a launch callable with the attributes of the reference
+callable (v7.py:475-487, :500-512) and its component kernels
+(direct_kernel, or partial_kernel + merge_kernel), so the reference harnesses'
+component timing (bench_split_breakdown.py:79-96) applies unchanged.
+"""
+from __future__ import annotations
+
+import ctypes
+from functools import lru_cache
+
+import torch
+
+from fgw_amd import _lib
+from fgw_amd.operators.mha import split_cost_model
+
+ROUTE = "hip_mfma"
+PERSISTENT_DEVICE = "device"  # cap the grid at the device's resident workgroups
+SPLIT_POLICIES = ("auto", "legacy", "cost_model")
+_DTYPES = {"float16": torch.float16, "bfloat16": torch.bfloat16}
+_LAYOUTS = {None: _lib.LAYOUT_AUTO, "query": _lib.LAYOUT_QUERY, "key": _lib.LAYOUT_KEY}
+
+
+def _dtype_name(dtype) -> str:
+    name = str(dtype).replace("torch.", "")
+    if name not in _DTYPES:
+        raise ValueError("matching FP16/BF16 Q/K/V required")
+    return name
+
+
+def route(dtype, dim, page_size, sq=1, causal=False):
+    """The single kernel route (cf. v7.py:20-29); raises for unsupported specs."""
+    name = str(dtype).replace("torch.", "")
+    if name not in _DTYPES:
+        raise ValueError("matching FP16/BF16 Q/K/V required")
+    if dim < 16 or dim > 256 or dim % 16:
+        raise ValueError("D must be in [16, 256] and divisible by 16")
+    if page_size <= 0:
+        raise ValueError("positive page size, whole pool pages and positive table width required")
+    return ROUTE
+
+
+@lru_cache(maxsize=8)
+def _device_info(index: int) -> _lib.DeviceInfo:
+    return _lib.query_device(index)
+
+
+def _persistent_request(persistent_programs) -> int:
+    if persistent_programs == PERSISTENT_DEVICE:
+        return -1
+    if persistent_programs is None:
+        return 0
+    if type(persistent_programs) is not int or persistent_programs < 1:
+        raise ValueError("persistent_programs supports None (uncapped grid), 'device' or a positive int")
+    return persistent_programs
+
+
+class _Launch:
+    """Launch callable of one static specialisation; see build_kernel."""
+
+    def __init__(self, shape: _lib.Shape, plan: _lib.Plan, device_index: int, dtype: torch.dtype,
+                 meta: dict):
+        self._shape = shape
+        self._plan = plan
+        self._device = torch.device("cuda", device_index)
+        self._dtype = dtype
+        self._out_shape = (shape.batch, shape.sq, shape.heads, shape.dim)
+        self._kv_shape = (shape.pool_rows, shape.heads, shape.dim)
+        self._meta_shapes = ((shape.batch, shape.width), (shape.batch,))
+        self._lib = _lib.load()
+        self.block_q = plan.rows_per_tile
+        self.compute_grid = plan.grid
+        self.task_assignment = "contiguous"
+        self.compute_work = plan.work_items
+        self.persistent_programs = meta["persistent_programs"]
+        self.requested_split_policy = meta["requested_split_policy"]
+        self.split_policy = meta["split_policy"]
+        self.num_splits = plan.num_splits
+        self.query_tile_tasks = plan.query_tile_tasks
+        self.execution_mode = "split_and_merge" if plan.execution_mode else "direct_single_split"
+        self.execution_path = ROUTE
+        self.layout = "key" if plan.layout == _lib.LAYOUT_KEY else "query"
+        self.dim_padded = plan.dim_padded
+        # Q is read in place as [B, Sq, H, D]; no head-major copy is needed.
+        self.prepare_q = lambda q: q
+        if plan.execution_mode == 0:
+            self.direct_kernel = self._direct
+        else:
+            self.partial_kernel = self._partial
+            self.merge_kernel = self._merge
+
+    # -- helpers -----------------------------------------------------------
+    def _check(self, q, k, v, table, lengths):
+        if (tuple(q.shape) != self._out_shape or tuple(k.shape) != self._kv_shape
+                or tuple(v.shape) != self._kv_shape or tuple(table.shape) != self._meta_shapes[0]
+                or tuple(lengths.shape) != self._meta_shapes[1]):
+            raise ValueError("tensor shapes do not match the built kernel")
+        if q.dtype != self._dtype or k.dtype != self._dtype or v.dtype != self._dtype:
+            raise ValueError("matching FP16/BF16 Q/K/V required")
+        if table.dtype != torch.int32 or lengths.dtype != torch.int32:
+            raise ValueError("int32 metadata required")
+        for x in (q, k, v, table, lengths):
+            if x.device != self._device or not x.is_contiguous():
+                raise ValueError("contiguous inputs on the same GPU required")
+
+    def _tensors(self, q, k, v, table, lengths, out=None, parts=None, lse=None):
+        return _lib.Tensors(q.data_ptr(), k.data_ptr(), v.data_ptr(), table.data_ptr(),
+                            lengths.data_ptr(), None if out is None else out.data_ptr(),
+                            None if parts is None else parts.data_ptr(),
+                            None if lse is None else lse.data_ptr())
+
+    def _stream(self):
+        return ctypes.c_void_p(torch.cuda.current_stream(self._device).cuda_stream)
+
+    def _workspace(self):
+        parts = torch.empty(self._plan.parts_floats, dtype=torch.float32, device=self._device)
+        lse = torch.empty(self._plan.lse_floats, dtype=torch.float32, device=self._device)
+        return parts, lse
+
+    # -- public calls --------------------------------------------------------
+    def __call__(self, q, k, v, table, lengths):
+        self._check(q, k, v, table, lengths)
+        out = torch.empty(self._out_shape, dtype=self._dtype, device=self._device)
+        parts = lse = None
+        if self._plan.execution_mode:
+            parts, lse = self._workspace()
+        t = self._tensors(q, k, v, table, lengths, out, parts, lse)
+        _lib.check(self._lib.fgw_mha_fwd(ctypes.byref(self._shape), ctypes.byref(self._plan),
+                                         ctypes.byref(t), self._stream()))
+        return out
+
+    def _direct(self, q, k, v, table, lengths):
+        return self(q, k, v, table, lengths)
+
+    def _partial(self, q, k, v, table, lengths):
+        """Partials [B, H, S, Sq, D] (O/l) and LSE [B, H, S, Sq]."""
+        self._check(q, k, v, table, lengths)
+        parts, lse = self._workspace()
+        t = self._tensors(q, k, v, table, lengths, None, parts, lse)
+        _lib.check(self._lib.fgw_mha_partial(ctypes.byref(self._shape), ctypes.byref(self._plan),
+                                             ctypes.byref(t), self._stream()))
+        s = self._shape
+        return (parts.view(s.batch, s.heads, self.num_splits, s.sq, s.dim),
+                lse.view(s.batch, s.heads, self.num_splits, s.sq))
+
+    def _merge(self, parts, lse):
+        s = self._shape
+        if (parts.dtype != torch.float32 or lse.dtype != torch.float32
+                or parts.numel() != self._plan.parts_floats or lse.numel() != self._plan.lse_floats
+                or not parts.is_contiguous() or not lse.is_contiguous()
+                or parts.device != self._device or lse.device != self._device):
+            raise ValueError("merge expects this kernel's contiguous fp32 partials and LSE")
+        out = torch.empty(self._out_shape, dtype=self._dtype, device=self._device)
+        t = _lib.Tensors(None, None, None, None, None, out.data_ptr(), parts.data_ptr(),
+                         lse.data_ptr())
+        _lib.check(self._lib.fgw_mha_merge(ctypes.byref(s), ctypes.byref(self._plan),
+                                           ctypes.byref(t), self._stream()))
+        return out
+
+
+@lru_cache(maxsize=128)
+def build_kernel(batch, sq, heads, dim, pool_rows, width, page_size, causal, dtype,
+                 device_index=None, num_splits=None, split_policy="auto", full_kv_cache=False,
+                 persistent_programs=PERSISTENT_DEVICE, cache_lengths=None, layout=None):
+    """Plan one static specialisation and return its launch callable.
+
+    Arguments follow the reference build_kernel (v7.py:32-47) plus
+    persistent_programs (v7_experimental.py:29-30: None = uncapped grid; here
+    the default caps the grid at the device's resident workgroups),
+    cache_lengths (host-known lengths for the cost model,
+    cube_general.py:17, :45) and layout ("query" = waves split query rows,
+    "key" = waves split key blocks; None chooses by Sq).
+    """
+    requested_split_policy = split_policy
+    if split_policy not in SPLIT_POLICIES:
+        raise ValueError("split_policy must be auto, legacy or cost_model")
+    if num_splits is not None and (type(num_splits) is not int or num_splits < 1
+                                   or num_splits & (num_splits - 1) or num_splits > 128):
+        raise ValueError("num_splits supports None (automatic) or 1/2/4/8/16/32/64/128")
+    name = _dtype_name(dtype)
+    route(name, dim, page_size, sq, causal)
+    if page_size <= 0 or pool_rows <= 0 or pool_rows % page_size or width <= 0:
+        raise ValueError("positive page size, whole pool pages and positive table width required")
+    if min(batch, sq, heads) <= 0:
+        raise ValueError("positive Q extents and rank-2 table required")
+    if device_index is None:
+        device_index = torch.cuda.current_device()
+    device = _device_info(int(device_index))
+    shape = _lib.Shape(batch, sq, heads, dim, pool_rows, width, page_size, int(bool(causal)),
+                       _lib.DTYPE_BFLOAT16 if name == "bfloat16" else _lib.DTYPE_FLOAT16)
+    persistent = _persistent_request(persistent_programs)
+    if layout not in _LAYOUTS:
+        raise ValueError("layout must be None, 'query' or 'key'")
+
+    if num_splits is not None:
+        splits, policy = num_splits, "explicit"
+    else:
+        if split_policy == "auto":
+            use_model = split_cost_model.eligible_config(
+                batch, sq, heads, dim, width * page_size, page_size=page_size, causal=causal,
+                full_kv_cache=full_kv_cache, num_cus=device.num_cus)
+            split_policy = "cost_model" if use_model else "legacy"
+        if split_policy == "cost_model":
+            lengths = cache_lengths
+            if lengths is None:
+                if not full_kv_cache:
+                    raise ValueError("Cost model requires full_kv_cache or host-known cache_lengths")
+                lengths = (width * page_size,) * batch
+            splits = split_cost_model.select_splits(batch, sq, heads, dim, width * page_size,
+                                                    tuple(lengths), device)
+        else:
+            splits = 0
+        policy = split_policy
+    plan = _lib.plan(shape, _lib.Request(splits, persistent, _LAYOUTS[layout]), device)
+    meta = {"persistent_programs": persistent_programs,
+            "requested_split_policy": requested_split_policy, "split_policy": policy}
+    return _Launch(shape, plan, int(device_index), _DTYPES[name], meta)
+
+
+def mha_paged_decode(q, k_cache, v_cache, block_table, cache_seqlens, page_size, is_causal=False,
+                     *, num_splits=None, split_policy="auto", persistent_programs=PERSISTENT_DEVICE):
+    """Paged attention forward; same tensor contract and checks as v7.py:516-570.
+
+    The cache lengths are copied to the host once to check
+    0 <= len <= W * page_size (the reference general route's check,
+    v7_experimental.py:870-873) and to detect a full cache for the split policy.
+    """
+    if q.ndim != 4 or k_cache.ndim != 3:
+        raise ValueError("expected Q[B,Sq,H,D], K/V[N,H,D]")
+    b, sq, h, d = q.shape
+    if min(b, sq, h, d) <= 0 or block_table.ndim != 2:
+        raise ValueError("positive Q extents and rank-2 table required")
+    if k_cache.shape[1:] != (h, d) or v_cache.shape != k_cache.shape:
+        raise ValueError("K/V shape mismatch")
+    if block_table.shape[0] != b or block_table.shape[1] <= 0 or cache_seqlens.shape != (b,):
+        raise ValueError("metadata shape mismatch")
+    if q.dtype not in (torch.float16, torch.bfloat16) or k_cache.dtype != q.dtype or v_cache.dtype != q.dtype:
+        raise ValueError("matching FP16/BF16 Q/K/V required")
+    if block_table.dtype != torch.int32 or cache_seqlens.dtype != torch.int32:
+        raise ValueError("int32 metadata required")
+    inputs = (q, k_cache, v_cache, block_table, cache_seqlens)
+    if q.device.type != "cuda" or any(x.device != q.device or not x.is_contiguous() for x in inputs):
+        raise ValueError("contiguous inputs on the same GPU required")
+    capacity = block_table.shape[1] * page_size
+    lengths = cache_seqlens.cpu().tolist()
+    if any(n < 0 or n > capacity for n in lengths):
+        raise ValueError("Cache lengths must be within table capacity")
+    full_kv_cache = all(n == capacity for n in lengths)
+    with torch.cuda.device(q.device):
+        kernel = build_kernel(b, sq, h, d, k_cache.shape[0], block_table.shape[1], page_size,
+                              bool(is_causal), "float16" if q.dtype == torch.float16 else "bfloat16",
+                              q.device.index, num_splits=num_splits, split_policy=split_policy,
+                              full_kv_cache=full_kv_cache, persistent_programs=persistent_programs,
+                              cache_lengths=tuple(lengths) if split_policy == "cost_model" else None)
+        return kernel(*inputs)

@@ -1,0 +1,101 @@
+"""Split-count selector refit for MI355X (256 CUs).
+
+Counterpart of the reference's frozen 28-core selectors
+(operators/mha/split_cost_model.py:13-44 and
+operators/mha/general_split_cost_model.py:44-91): a linear latency model over
+per-candidate features, with weights fitted on MI355X split scans and frozen
+in split_cost_model.json. Pure Python, no device calls. Scores rank split
+candidates; the smallest split within the selection tolerance of the best
+predicted latency wins (less workspace and merge work), as in
+general_split_cost_model.py:152-156.
+
+Features of candidate s (layout and keys-per-round as the C planner uses:
+Sq <= 32 -> 4 key-parallel waves over 32 query rows, 128 keys per round;
+else 4 query-parallel waves over 128 rows, 64 keys per round):
+  constant
+  wave_rounds      programs waves x key rounds of the longest split  (critical path)
+  waves            ceil(tasks * s / resident slots)
+  has_merge        s > 1
+  partial_mbytes   s > 1: fp32 partial + LSE bytes written and read back, in MB
+  merge_rows       s > 1: output rows merged x s / 1e3
+  longest_excess   key rounds of the longest request's split beyond the mean
+                   (ragged batches; general_split_cost_model.py:128-131)
+"""
+from __future__ import annotations
+
+import json
+import math
+import pathlib
+from functools import lru_cache
+from typing import Optional, Sequence
+
+MODEL_PATH = pathlib.Path(__file__).with_name("split_cost_model.json")
+SPLITS = (1, 2, 4, 8, 16, 32, 64)
+FEATURE_NAMES = ("constant", "wave_rounds", "waves", "has_merge", "partial_mbytes", "merge_rows",
+                 "longest_excess")
+
+
+def geometry(sq: int):
+    """(layout index, rows per tile, keys per round) of the planner's layout choice."""
+    return (1, 32, 128) if sq <= 32 else (0, 128, 64)
+
+
+def features(batch, sq, heads, dim, lengths: Sequence[int], splits, num_cus, wg_per_cu):
+    layout, rows, keys_round = geometry(sq)
+    tasks = batch * heads * math.ceil(sq / rows)
+    slots = max(1, num_cus * max(1, wg_per_cu[layout]))
+    waves = math.ceil(tasks * splits / slots)
+    rounds = [math.ceil(n / keys_round) for n in lengths]
+    longest = math.ceil(max(rounds) / splits) if rounds else 0
+    mean = (sum(rounds) / len(rounds)) / splits if rounds else 0.0
+    multi = int(splits > 1)
+    parts_mb = multi * batch * heads * splits * sq * (dim + 1) * 4 * 2 / 1e6
+    return [1.0, waves * longest * dim / 128.0, float(waves), float(multi), parts_mb,
+            multi * batch * heads * sq * splits / 1e3, max(0.0, longest - mean)]
+
+
+@lru_cache(maxsize=2)
+def load_model(path: str = str(MODEL_PATH)) -> Optional[dict]:
+    """The frozen MI355X model, or None when no calibration has been committed."""
+    p = pathlib.Path(path)
+    if not p.exists():
+        return None
+    model = json.loads(p.read_text(encoding="utf-8"))
+    if model.get("feature_names") != list(FEATURE_NAMES) or len(model["weights"]) != len(FEATURE_NAMES):
+        raise ValueError("split cost model feature mismatch")
+    if any(not math.isfinite(w) or w < 0 for w in model["weights"]):
+        raise ValueError("split cost model requires finite nonnegative weights")
+    return model
+
+
+def eligible_config(batch, sq, heads, dim, kv_tokens, *, page_size, causal, full_kv_cache,
+                    num_cus) -> bool:
+    """Automatic policy guard: the calibrated scope of the frozen model."""
+    model = load_model()
+    if model is None:
+        return False
+    scope = model["scope"]
+    return (not causal and num_cus == scope["num_cus"] and full_kv_cache
+            and scope["min_kv"] <= kv_tokens <= scope["max_kv"]
+            and scope["min_sq"] <= sq <= scope["max_sq"] and dim in scope["dims"])
+
+
+def predict(batch, sq, heads, dim, lengths, splits, num_cus, wg_per_cu, model) -> float:
+    x = features(batch, sq, heads, dim, lengths, splits, num_cus, wg_per_cu)
+    return sum(w * v for w, v in zip(model["weights"], x))
+
+
+def select_splits(batch, sq, heads, dim, capacity_tokens, lengths, device, model=None) -> int:
+    """Split count with the lowest predicted latency (ties -> fewer splits)."""
+    model = model or load_model()
+    if model is None:
+        raise ValueError("No MI355X split cost model calibration is available; use split_policy='legacy'")
+    if len(lengths) != batch or any(n < 0 or n > capacity_tokens for n in lengths):
+        raise ValueError("cache_lengths must match batch and page-table capacity")
+    wg = tuple(device.wg_per_cu)
+    max_split = max(1, math.ceil(capacity_tokens / 32))
+    costs = {s: predict(batch, sq, heads, dim, lengths, s, device.num_cus, wg, model)
+             for s in SPLITS if s <= max_split}
+    best = min(costs.values())
+    limit = best + max(abs(best) * model["selection_tolerance"], model.get("absolute_margin_us", 0.0))
+    return min(s for s, c in costs.items() if c <= limit)

@@ -1,0 +1,167 @@
+/*
+ * fgw_mha.h -- C ABI of the MI355X (gfx950) paged multi-head attention operator.
+ *
+ * Drop-in boundary for the reference operator entry `operators/mha/current.py`
+ * (zhangwenhao91/FGW), which re-exports
+ * `operators/mha/kernels/mha_paged_decode_ascend_v7.py`:
+ *   mha_paged_decode(q, k_cache, v_cache, block_table, cache_seqlens, page_size,
+ *                    is_causal=False, *, num_splits=None, split_policy="auto")
+ *   build_kernel(batch, sq, heads, dim, pool_rows, width, page_size, causal, dtype, ...)
+ * The reference has no native FFI of its own: its kernels are TileLang JIT
+ * adapters. Every entry point below replaces one piece of that Python path,
+ * cited per declaration. The Python mirror of the reference interface
+ * (fgw_amd/operators/mha/current.py) binds these symbols through ctypes.
+ *
+ * Tensor contract (v0.py:107-122, v7.py:529-544):
+ *   Q, O      [B, Sq, H, D]   fp16 or bf16, contiguous
+ *   K, V      [N, H, D]       same dtype, N = pool rows (whole pages)
+ *   table     [B, W]          int32 page ids
+ *   lengths   [B]             int32 live cache length per request
+ * Query row q of request b sees keys [0, len_b) (non-causal) or
+ * [0, max(len_b - Sq + q + 1, 0)) (right-aligned causal, cube_general.py:121-126).
+ * Rows with no visible key are exactly zero.
+ *
+ * All functions return 0 on success or a negative fgw_mha_status; the message
+ * of the last failure on the calling thread is in fgw_mha_last_error().
+ * No function allocates, frees or synchronises device memory; launches are
+ * asynchronous on the given stream. Functions are reentrant.
+ */
+#ifndef FGW_MHA_H_
+#define FGW_MHA_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FGW_MHA_ABI_VERSION 1
+
+typedef enum {
+  FGW_MHA_OK = 0,
+  FGW_MHA_EINVAL = -1,      /* invalid argument (Python: ValueError) */
+  FGW_MHA_EUNSUPPORTED = -2, /* shape/dtype outside the kernel family (ValueError) */
+  FGW_MHA_EHIP = -3          /* HIP runtime error (RuntimeError) */
+} fgw_mha_status;
+
+typedef enum { FGW_MHA_FLOAT16 = 0, FGW_MHA_BFLOAT16 = 1 } fgw_mha_dtype;
+
+typedef enum {
+  FGW_MHA_LAYOUT_AUTO = -1,
+  FGW_MHA_LAYOUT_QUERY = 0, /* 4 waves x 32 query rows share 64-key K/V tiles (prefill) */
+  FGW_MHA_LAYOUT_KEY = 1    /* 4 waves split the keys of 32 query rows (decode) */
+} fgw_mha_layout;
+
+/* Static shape of one operator instance: the arguments of the reference
+ * build_kernel (v7.py:32-47) that fix a specialisation. */
+typedef struct {
+  int32_t batch;     /* B */
+  int32_t sq;        /* queries per request */
+  int32_t heads;     /* H */
+  int32_t dim;       /* D, 16..256, multiple of 16 */
+  int64_t pool_rows; /* N = pool pages * page_size */
+  int32_t width;     /* W, page-table width */
+  int32_t page_size; /* tokens per page, >= 1, N % page_size == 0 */
+  int32_t causal;    /* 0 / 1 */
+  int32_t dtype;     /* fgw_mha_dtype */
+} fgw_mha_shape;
+
+/* Planning request: the reference's split and persistent-grid controls
+ * (v7.py:43-46, :94-113; v7_experimental.py:29-30 persistent_programs). */
+typedef struct {
+  int32_t num_splits;          /* 0 = automatic; else 1,2,4,...,128 */
+  int32_t persistent_programs; /* -1 = CU-derived cap, 0 = uncapped grid, n > 0 = cap */
+  int32_t layout;              /* fgw_mha_layout */
+} fgw_mha_request;
+
+/* Device facts the planner needs; filled by fgw_mha_query_device. */
+typedef struct {
+  int32_t num_cus;          /* compute units */
+  int32_t wg_per_cu[2];     /* resident workgroups per CU, per layout, for dim = 128 */
+  int32_t arch_gfx950;      /* 1 when the device is gfx950 */
+} fgw_mha_device_info;
+
+/* Resolved launch plan: the attributes the reference launch callable
+ * exposes (v7.py:475-487, :500-512) plus workspace sizes. */
+typedef struct {
+  int32_t layout;          /* fgw_mha_layout actually used */
+  int32_t rows_per_tile;   /* query rows per work item (reference block_q) */
+  int32_t q_tiles;         /* ceil(Sq / rows_per_tile) */
+  int32_t num_splits;      /* KV splits per (b, h, q tile) */
+  int32_t query_tile_tasks;/* B * H * q_tiles */
+  int32_t work_items;      /* query_tile_tasks * num_splits (compute_work) */
+  int32_t grid;            /* launched programs (compute_grid) */
+  int32_t threads;         /* threads per program */
+  int32_t execution_mode;  /* 0 = direct single split, 1 = split and merge */
+  int32_t dim_padded;      /* head-dim tile of the selected kernel */
+  int64_t parts_floats;    /* fp32 elements of the partial-output workspace (0 if direct) */
+  int64_t lse_floats;      /* fp32 elements of the LSE workspace (0 if direct) */
+} fgw_mha_plan_t;
+
+/* Device buffers of one call. Workspaces are owned by the caller and sized
+ * from the plan; they are unused (may be NULL) for execution_mode 0. */
+typedef struct {
+  const void* q;
+  const void* k_cache;
+  const void* v_cache;
+  const int32_t* block_table;
+  const int32_t* cache_seqlens;
+  void* out;
+  float* parts; /* [B, H, S, Sq, D] */
+  float* lse;   /* [B, H, S, Sq]    natural-log sum-exp, -1e30 for an empty split */
+} fgw_mha_tensors;
+
+/* ABI version of the loaded library (FGW_MHA_ABI_VERSION). No reference
+ * counterpart. */
+int fgw_mha_abi_version(void);
+
+/* Message of the last failure on this thread ("" if none). No reference
+ * counterpart (the reference raises Python exceptions). */
+const char* fgw_mha_last_error(void);
+
+/* CU count and per-layout occupancy of a device. Replaces the reference's
+ * torch.npu.get_device_properties(...).cube_core_num reads (v7.py:64-68, :104-108). */
+int fgw_mha_query_device(int device, fgw_mha_device_info* info);
+
+/* Validate a shape and resolve layout, split count and grid. Pure host
+ * function (no HIP calls). Replaces the split selection and persistent-grid
+ * arithmetic of build_kernel (v7.py:48-113; general_split_policy.py:9-21):
+ * automatic splits double while B*H*q_tiles*splits leaves CU slots idle and
+ * every split keeps at least two rounds of key blocks. Errors mirror the
+ * reference ValueErrors (v7.py:49-55, :97-99). */
+int fgw_mha_plan(const fgw_mha_shape* shape, const fgw_mha_request* request,
+                 const fgw_mha_device_info* device, fgw_mha_plan_t* plan);
+
+/* Full forward: the direct kernel with the fused normalise/cast/store
+ * epilogue when num_splits == 1, else partial + merge. Replaces the compiled
+ * launch callable returned by build_kernel (v7.py:471-473, :495-498). */
+int fgw_mha_fwd(const fgw_mha_shape* shape, const fgw_mha_plan_t* plan,
+                const fgw_mha_tensors* t, hipStream_t stream);
+
+/* Partial kernel only: writes parts[b,h,s,q,:] = O_s / l_s and lse[b,h,s,q].
+ * Replaces launch.partial_kernel (v7.py:225-315, :488-490), the component the
+ * reference's split breakdown times as "local" (bench_split_breakdown.py:79-96). */
+int fgw_mha_partial(const fgw_mha_shape* shape, const fgw_mha_plan_t* plan,
+                    const fgw_mha_tensors* t, hipStream_t stream);
+
+/* LSE merge only: reads parts/lse, writes out. Replaces launch.merge_kernel
+ * (v7.py:317-371, :491-493). */
+int fgw_mha_merge(const fgw_mha_shape* shape, const fgw_mha_plan_t* plan,
+                  const fgw_mha_tensors* t, hipStream_t stream);
+
+/* Gather the live K/V rows of every request into packed [B, out_len, H, D]
+ * buffers (zero rows past len). Uses the attention kernel's page resolution
+ * table[b, pos // page] * page + pos % page (v0.py:137); replaces the paged
+ * cache gather the reference validates row-exactly
+ * (benchmarks/mha/external_cache_gather.py:55-64). */
+int fgw_mha_gather_kv(const fgw_mha_shape* shape, const fgw_mha_tensors* t, void* out_k,
+                      void* out_v, int32_t out_len, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FGW_MHA_H_ */

@@ -1,0 +1,129 @@
+"""C ABI and host logic, CPU only: the library loads, exports every declared
+symbol, and its planner/validation behave as specified (no kernel launches)."""
+import ctypes
+import pathlib
+import re
+
+import pytest
+import torch
+
+from fgw_amd import _lib
+
+ROOT = pathlib.Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "fgw_mha.h"
+DEVICE = _lib.DeviceInfo(256, (ctypes.c_int32 * 2)(2, 2), 1)
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _lib.LIBRARY.exists():
+        from fgw_amd import build
+        build.build(verbose=False)
+    return _lib.load()
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\w[\w\s\*]*?\b(fgw_mha_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_every_declared_symbol_is_exported(lib):
+    names = declared_functions()
+    assert len(names) == 8, names
+    for name in names:
+        assert hasattr(lib, name), name
+    assert set(names) == set(_lib.SIGNATURES)
+    assert lib.fgw_mha_abi_version() == _lib.ABI_VERSION
+
+
+def shape(b=2, sq=1, h=8, d=128, kv=32768, page=128, causal=0, dtype=_lib.DTYPE_BFLOAT16):
+    width = (kv + page - 1) // page
+    return _lib.Shape(b, sq, h, d, b * width * page, width, page, causal, dtype)
+
+
+def test_plan_headline_shapes(lib):
+    prefill = _lib.plan(shape(sq=4096, kv=2048), _lib.Request(0, -1, -1), DEVICE)
+    assert (prefill.layout, prefill.rows_per_tile, prefill.q_tiles, prefill.num_splits) == (0, 128, 32, 1)
+    assert (prefill.work_items, prefill.grid, prefill.execution_mode) == (512, 512, 0)
+    decode = _lib.plan(shape(sq=1, kv=32768), _lib.Request(0, -1, -1), DEVICE)
+    assert (decode.layout, decode.rows_per_tile, decode.num_splits, decode.work_items) == (1, 32, 32, 512)
+    assert decode.parts_floats == 2 * 8 * 32 * 1 * 128 and decode.lse_floats == 2 * 8 * 32
+    big = _lib.plan(shape(sq=32768, kv=2048), _lib.Request(0, -1, -1), DEVICE)
+    assert big.work_items == 2 * 8 * 256 and big.grid == 512  # persistent cap = 256 CUs x 2
+    uncapped = _lib.plan(shape(sq=32768, kv=2048), _lib.Request(0, 0, -1), DEVICE)
+    assert uncapped.grid == uncapped.work_items
+    capped = _lib.plan(shape(sq=32768, kv=2048), _lib.Request(0, 28, -1), DEVICE)
+    assert capped.grid == 28
+
+
+def test_plan_split_rules(lib):
+    # Auto splits never leave a split with fewer than two rounds of key blocks.
+    small = _lib.plan(shape(sq=1, kv=512), _lib.Request(0, -1, -1), DEVICE)
+    assert small.num_splits == 2
+    tiny = _lib.plan(shape(sq=1, kv=128), _lib.Request(0, -1, -1), DEVICE)
+    assert tiny.num_splits == 1 and tiny.execution_mode == 0
+    explicit = _lib.plan(shape(sq=16, kv=8192), _lib.Request(16, -1, -1), DEVICE)
+    assert explicit.num_splits == 16 and explicit.execution_mode == 1
+    forced = _lib.plan(shape(sq=64, kv=8192), _lib.Request(0, -1, _lib.LAYOUT_KEY), DEVICE)
+    assert (forced.layout, forced.q_tiles) == (1, 2)
+    for bad in (3, 256, -2):
+        with pytest.raises(ValueError, match="num_splits"):
+            _lib.plan(shape(), _lib.Request(bad, -1, -1), DEVICE)
+    with pytest.raises(ValueError, match="KV tiles"):
+        _lib.plan(shape(kv=128), _lib.Request(8, -1, -1), DEVICE)
+
+
+@pytest.mark.parametrize("field,value,message", [
+    ("dim", 24, "divisible by 16"),
+    ("dim", 272, "D must be"),
+    ("page_size", 0, "positive page size"),
+    ("pool_rows", 1000, "whole pool pages"),
+    ("dtype", 7, "FP16/BF16"),
+    ("sq", 0, "positive Q extents"),
+])
+def test_plan_rejects_invalid_shapes(lib, field, value, message):
+    s = shape()
+    setattr(s, field, value)
+    with pytest.raises(ValueError, match=message):
+        _lib.plan(s, _lib.Request(0, -1, -1), DEVICE)
+
+
+def test_fwd_rejects_null_and_misaligned_buffers(lib):
+    s = shape(sq=4, kv=512)
+    p = _lib.plan(s, _lib.Request(1, -1, -1), DEVICE)
+    t = _lib.Tensors()
+    rc = lib.fgw_mha_fwd(ctypes.byref(s), ctypes.byref(p), ctypes.byref(t), None)
+    assert rc == _lib.FGW_MHA_EINVAL and b"NULL" in lib.fgw_mha_last_error()
+    t = _lib.Tensors(16, 32, 48, 64, 80, 97, None, None)
+    rc = lib.fgw_mha_fwd(ctypes.byref(s), ctypes.byref(p), ctypes.byref(t), None)
+    assert rc == _lib.FGW_MHA_EINVAL and b"aligned" in lib.fgw_mha_last_error()
+    p.grid = 0  # a plan that does not match the shape is rejected before any launch
+    rc = lib.fgw_mha_fwd(ctypes.byref(s), ctypes.byref(p), ctypes.byref(t), None)
+    assert rc == _lib.FGW_MHA_EINVAL and b"plan" in lib.fgw_mha_last_error()
+
+
+def test_public_validation_matches_reference_messages():
+    from fgw_amd.operators.mha.current import build_kernel, mha_paged_decode
+    q = torch.zeros(1, 1, 2, 16, dtype=torch.bfloat16)
+    k = torch.zeros(32, 2, 16, dtype=torch.bfloat16)
+    table = torch.zeros(1, 2, dtype=torch.int32)
+    lengths = torch.zeros(1, dtype=torch.int32)
+    cases = [
+        ((q[0], k, k, table, lengths, 16), "expected Q\\[B,Sq,H,D\\]"),
+        ((q, k[:, :1], k, table, lengths, 16), "K/V shape mismatch"),
+        ((q, k, k, table[:, :0], lengths, 16), "metadata shape mismatch"),
+        ((q.half(), k, k, table, lengths, 16), "matching FP16/BF16"),
+        ((q, k, k, table.long(), lengths, 16), "int32 metadata"),
+        ((q, k, k, table, lengths, 16), "same GPU"),  # CPU tensors
+    ]
+    for args, message in cases:
+        with pytest.raises(ValueError, match=message):
+            mha_paged_decode(*args)
+    with pytest.raises(TypeError):
+        mha_paged_decode(q, k, k, table, lengths, 16, cube_mode="general")
+    with pytest.raises(ValueError, match="split_policy"):
+        build_kernel(1, 1, 2, 16, 32, 2, 16, False, "bfloat16", 0, split_policy="fastest")
+    with pytest.raises(ValueError, match="num_splits"):
+        build_kernel(1, 1, 2, 16, 32, 2, 16, False, "bfloat16", 0, num_splits=3)
+    with pytest.raises(ValueError, match="D must be"):
+        build_kernel(1, 1, 2, 24, 32, 2, 16, False, "bfloat16", 0)

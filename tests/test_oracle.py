@@ -1,0 +1,233 @@
+"""Pins of the CPU oracle (oracle/mha_oracle.py) -- CPU only.
+
+Each oracle function is checked against something that does not restate it:
+the reference's recorded harness vectors, a float64 brute force written with
+plain Python loops, closed forms, the reference's own merge vectors and
+published counts. Planted mistakes in copies of the oracle must fail the
+same checks.
+"""
+import json
+import math
+import pathlib
+import random
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import mha_oracle as O
+from tests import mha_cases
+
+GOLDEN = pathlib.Path(__file__).with_name("golden") / "accuracy_report_vectors.json"
+
+
+# ---------------------------------------------------------------- input recipes
+def test_lengths_and_pool_rows_match_reference_reports():
+    vectors = json.loads(GOLDEN.read_text())["vectors"]
+    assert len(vectors) >= 200
+    for vec in vectors:
+        case = (vec["case"], vec["B"], vec["Sq"], vec["H"], vec["D"], vec["page_size"],
+                vec["table_width"])
+        assert O.lengths_for(case, vec["pattern"], vec["seed"]) == vec["lengths"], vec
+        pool_pages = max(case[6] + 3, case[1] * case[6] + 1)
+        assert pool_pages * case[5] == vec["pool_rows"], vec
+
+
+def test_make_inputs_recipe_properties():
+    for name in ("tiny", "many_queries", "general_d48_page48", "split_d16_q1"):
+        case = mha_cases.ALL_CASES[name]
+        _, b, sq, h, d, p, w = case
+        q, k, v, table = O.make_inputs(case, 7, torch.bfloat16)
+        pool_pages = max(w + 3, b * w + 1)
+        assert q.shape == (b, sq, h, d) and k.shape == (pool_pages * p, h, d) == v.shape
+        assert table.dtype == torch.int32 and table.shape == (b, w)
+        assert int(table.max()) < pool_pages - 1  # the last pool page is never referenced
+        if b > 1:
+            assert (table[1:, 0] == table[0, 0]).all()
+        if w > 1:
+            assert table[-1, -1] == table[-1, 0]
+        q2, _, _, table2 = O.make_inputs(case, 7, torch.bfloat16)
+        assert torch.equal(q, q2) and torch.equal(table, table2)  # seeded
+
+
+def test_poison_unread_marks_exactly_the_dead_rows():
+    case = mha_cases.ALL_CASES["many_queries"]
+    q, k, v, table = O.make_inputs(case, 42, torch.float16)
+    lengths = torch.tensor(O.lengths_for(case, "mixed", 42), dtype=torch.int32)
+    kp, vp = O.poison_unread(k, v, table, lengths, case[5])
+    live = set()
+    for b in range(table.shape[0]):
+        for pos in range(int(lengths[b])):
+            live.add(int(table[b, pos // case[5]]) * case[5] + pos % case[5])
+    for row in range(k.shape[0]):
+        assert bool(torch.isnan(kp[row]).all()) == (row not in live)
+        assert bool(torch.isnan(vp[row]).all()) == (row not in live)
+
+
+# ------------------------------------------------------------- float64 brute force
+def brute_force(q, k, v, table, lengths, page, causal):
+    """Softmax attention in float64 with explicit Python loops."""
+    q64, k64, v64 = (x.double().numpy() for x in (q, k, v))
+    b_, sq, h_, d = q64.shape
+    out = np.zeros((b_, sq, h_, d))
+    for b in range(b_):
+        n = int(lengths[b])
+        rows = [int(table[b, pos // page]) * page + pos % page for pos in range(n)]
+        for qi in range(sq):
+            end = max(n - sq + qi + 1, 0) if causal else n
+            for hh in range(h_):
+                if end == 0:
+                    continue
+                scores = [sum(q64[b, qi, hh, x] * k64[r, hh, x] for x in range(d)) / math.sqrt(d)
+                          for r in rows[:end]]
+                peak = max(scores)
+                w = [math.exp(s - peak) for s in scores]
+                tot = sum(w)
+                for x in range(d):
+                    out[b, qi, hh, x] = sum(wi * v64[r, hh, x] for wi, r in zip(w, rows[:end])) / tot
+    return torch.from_numpy(out)
+
+
+def tiny_problem(seed, b=3, sq=4, h=2, d=16, page=3, width=4, lengths=(0, 2, 11), dtype=torch.float32):
+    g = torch.Generator().manual_seed(seed)
+    pages = b * width + 2
+    table = torch.randperm(pages, generator=g)[: b * width].reshape(b, width).to(torch.int32)
+    table[-1, -1] = table[-1, 0]
+    q = torch.randn(b, sq, h, d, generator=g).to(dtype)
+    k = torch.randn(pages * page, h, d, generator=g).to(dtype)
+    v = torch.randn(pages * page, h, d, generator=g).to(dtype)
+    return q, k, v, table, torch.tensor(lengths, dtype=torch.int32), page
+
+
+@pytest.mark.parametrize("seed", [1, 2, 3])
+@pytest.mark.parametrize("causal", [False, True])
+def test_reference_matches_float64_brute_force(seed, causal):
+    q, k, v, table, lengths, page = tiny_problem(seed)
+    expected = brute_force(q, k, v, table, lengths, page, causal)
+    for fn in (O.reference, lambda *a: O.chunked_reference(*a, chunk=3)):
+        got = fn(q, k, v, table, lengths, page, causal)
+        torch.testing.assert_close(got.double(), expected, rtol=1e-5, atol=1e-6)
+
+
+def test_reference_closed_forms():
+    q, k, v, table, lengths, page = tiny_problem(5, lengths=(1, 0, 7))
+    out = O.reference(q, k, v, table, lengths, page, False)
+    row0 = int(table[0, 0]) * page
+    torch.testing.assert_close(out[0, :, :, :], v[row0].expand_as(out[0]), rtol=0, atol=1e-6)
+    assert torch.count_nonzero(out[1]) == 0
+    # Equal keys give equal weights: the output is the mean of the visible V rows.
+    k2 = k.clone()
+    k2[:] = k[0]
+    out = O.reference(q, k2, v, table, lengths, page, False)
+    rows = O.physical_rows(table, 2, 7, page)
+    torch.testing.assert_close(out[2, 0], v[rows].mean(0), rtol=1e-5, atol=1e-6)
+    # Causal, Sq > len: rows with no visible key are exactly zero.
+    out = O.reference(q, k, v, table, lengths, page, True)
+    assert torch.count_nonzero(out[0, :3]) == 0 and torch.count_nonzero(out[0, 3]) > 0
+
+
+def test_chunked_reference_equals_reference_at_bf16():
+    case = mha_cases.ALL_CASES["cube_q129"]
+    q, k, v, table = O.make_inputs(case, 7, torch.bfloat16)
+    for causal in (False, True):
+        lengths = torch.tensor(O.lengths_for(case, "mixed", 7), dtype=torch.int32)
+        a = O.reference(q, k, v, table, lengths, case[5], causal)
+        b = O.chunked_reference(q, k, v, table, lengths, case[5], causal, 32)
+        torch.testing.assert_close(a, b, rtol=1e-2, atol=4e-3)
+
+
+# Planted mistakes: each must be caught by the brute-force pin.
+def _wrong_scale(q, k, v, table, lengths, page, causal):
+    return O.reference(q * math.sqrt(q.shape[-1]) ** 0.5, k, v, table, lengths, page, causal)
+
+
+def _wrong_causal(q, k, v, table, lengths, page, causal):
+    return O.reference(q, k, v, table, lengths + 1, page, causal)
+
+
+def _wrong_page(q, k, v, table, lengths, page, causal):
+    return O.reference(q, k, v, table.flip(1).contiguous(), lengths, page, causal)
+
+
+def _wrong_operand(q, k, v, table, lengths, page, causal):
+    return O.reference(q, v, k, table, lengths, page, causal)
+
+
+@pytest.mark.parametrize("mutant", [_wrong_scale, _wrong_causal, _wrong_page, _wrong_operand])
+def test_planted_mistakes_fail_the_pin(mutant):
+    q, k, v, table, lengths, page = tiny_problem(9, lengths=(5, 9, 11))
+    expected = brute_force(q, k, v, table, lengths, page, True)
+    got = mutant(q, k, v, table, lengths.clone(), page, True)
+    assert not torch.allclose(got.double(), expected, rtol=1e-3, atol=1e-4)
+
+
+# ------------------------------------------------------------------- split merge
+def test_merge_matches_reference_raw_partition_vectors():
+    # Vectors of tests/mha/test_raw_partial_state.py:8-10 (2-D keys/values).
+    keys = [(1., 2.), (-3., 4.), (5., -6.), (2., -1.), (-4., -2.), (3., 5.)]
+    values = [(2., -1.), (4., 3.), (-2., 5.), (7., -3.), (1., 6.), (-5., 8.)]
+    for query in ((1., -2.), (-3., 4.), (100., -100.)):
+        scores = [sum(a * b for a, b in zip(query, key)) / math.sqrt(2) for key in keys]
+        peak = max(scores)
+        w = [math.exp(x - peak) for x in scores]
+        dense = [sum(wi * val[d] for wi, val in zip(w, values)) / sum(w) for d in range(2)]
+        parts, lse = [], []
+        for begin, end in ((0, 2), (2, 5), (5, 6), (6, 6)):
+            if begin == end:
+                parts.append([0.0, 0.0])
+                lse.append(-1e30)
+                continue
+            m = max(scores[begin:end])
+            ww = [math.exp(x - m) for x in scores[begin:end]]
+            parts.append([sum(a * val[d] for a, val in zip(ww, values[begin:end])) / sum(ww)
+                          for d in range(2)])
+            lse.append(m + math.log(sum(ww)))
+        p = torch.tensor(parts, dtype=torch.float64).reshape(1, 1, 4, 1, 2)
+        s = torch.tensor(lse, dtype=torch.float64).reshape(1, 1, 4, 1)
+        got = O.merge_partials(p, s, torch.float64)
+        torch.testing.assert_close(got.reshape(2).double(), torch.tensor(dense, dtype=torch.float64),
+                                   rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("splits", [1, 2, 3, 8])
+@pytest.mark.parametrize("causal", [False, True])
+def test_partial_states_merge_to_dense(splits, causal):
+    q, k, v, table, lengths, page = tiny_problem(11, sq=5, lengths=(0, 4, 12))
+    parts, lse = O.partial_states(q, k, v, table, lengths, page, causal, splits, block_keys=2,
+                                  rows_per_tile=2)
+    got = O.merge_partials(parts, lse, torch.float32)
+    expected = brute_force(q, k, v, table, lengths, page, causal)
+    torch.testing.assert_close(got.double(), expected, rtol=1e-5, atol=1e-6)
+    empty = lse <= -1e29
+    assert torch.count_nonzero(parts[empty.unsqueeze(-1).expand_as(parts)]) == 0
+
+
+# ------------------------------------------------------------ counts and helpers
+def test_useful_flops_and_bytes_known_answers():
+    assert O.useful_flops([2048, 2048], 4096, 8, 128, False) == 68_719_476_736
+    assert O.useful_flops([2048, 2048], 32768, 8, 128, False) == 549_755_813_888
+    assert O.algorithmic_bytes([32768, 32768], 1, 8, 128, 256) == 268_445_704
+    # Causal square attention counts S(S+1)/2 pairs (MFU.md section 4).
+    assert O.useful_flops([100], 100, 1, 16, True) == 4 * 16 * 100 * 101 // 2
+
+
+def test_page_division_is_exact():
+    rng = random.Random(3)
+    for page in list(range(1, 300)) + [1000, 4096, 65535, 2**20 + 7]:
+        magic, shift = O.page_divisor(page)
+        assert 0 <= magic < 2**32
+        ns = list(range(0, 3000)) + [rng.randrange(0, 2**31) for _ in range(300)] + [2**31 - 1]
+        for n in ns:
+            assert O.page_div(n, magic, shift) == n // page, (page, n)
+
+
+def test_gather_packed_matches_explicit_rows():
+    q, k, v, table, lengths, page = tiny_problem(4, lengths=(3, 0, 10))
+    ok, ov = O.gather_packed(k, v, table, lengths, page, out_len=12)
+    for b in range(3):
+        for pos in range(12):
+            if pos < int(lengths[b]):
+                row = int(table[b, pos // page]) * page + pos % page
+                assert torch.equal(ok[b, pos], k[row]) and torch.equal(ov[b, pos], v[row])
+            else:
+                assert torch.count_nonzero(ok[b, pos]) == 0
