@@ -22,6 +22,9 @@ ARCH = "gfx950"
 HIP_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in VGPRs: the softmax and rescale read them with
+    # plain VALU ops instead of v_accvgpr copies.
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 
 

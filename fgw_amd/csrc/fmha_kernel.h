@@ -1,33 +1,43 @@
 // Paged multi-head attention forward for CDNA4 (gfx950).
 //
-// One templated kernel covers decode and long-Q prefill, FP16/BF16 and
-// head dims 16..256. It computes, per (request b, head h, query tile,
+// One templated kernel covers decode and long-Q prefill, FP16/BF16 and head
+// dims 16..256. It computes, per work item (request b, head h, query tile,
 // KV split), the online-softmax attention of the tile's query rows against
-// the visible keys of the split, reading K/V rows through the block table.
+// the split's visible keys, reading K/V rows through the block table.
 //
 // Math follows the reference operator (operators/mha/kernels/
 // mha_paged_decode_ascend_v7.py:120-205, :305-315; cube_general.py:88-157):
 //   s = q.k * D^-0.5, running max m, p = exp(s - m) rounded to the input dtype
 //   for the PV product, l = l*alpha + sum(p) in fp32, O = alpha*O + P.V,
 //   output O / max(l, 1e-30); partial mode stores O/l and LSE = ln(l) + m.
-// The exponentials run as exp2 on log2(e)-prescaled scores.
+// The exponentials run as exp2 on log2(e)-prescaled scores. The head dim is
+// padded with zeros to a power of two >= 32 (as cube_general.py:31 does);
+// the scale uses the true D.
+//
+// Data path per 64-key (prefill) or 32-key (decode) block:
+//   HBM -> LDS by global_load_lds_dwordx4 (DMA, no staging registers). K and
+//   V tiles are row-major [key][d] with XOR-swizzled 16-byte chunks. Lanes
+//   whose chunk is masked (key >= len, d >= D, page id outside the pool) load
+//   a global zero chunk instead, so loads are branch-free and unread cache
+//   rows (possibly NaN) never reach the products (cube_general.py:97-109).
+//   LDS -> MFMA operands by ds_read_b128 (K) and ds_read_b64_tr_b16 (V: the
+//   transposing read yields V^T operand columns straight from row-major V).
 //
 // Matrix-core formulation (v_mfma_f32_32x32x16_{bf16,f16}, wave64):
-//   S^T = K . Q^T   A = K tile rows (keys) from LDS, B = Q^T held in VGPRs.
-//                   The 32x32 accumulator gives each lane one query column
-//                   (lane % 32) and 16 key rows.
-//   O^T = V^T . P^T A = V^T rows (head dim) from LDS, B = P^T straight from
-//                   the S^T accumulator registers after the softmax: the
-//                   16 keys a lane holds are exactly the k-slots of its B
-//                   operand once V^T is stored with 4-key groups 1 and 2 of
-//                   every 16-key group swapped.
-// So every lane owns one query row in both products: the softmax needs one
-// cross-half (lane ^ 32) exchange per block for the max and the rescale of O
+//   S^T = K . Q^T   A = K rows from LDS, B = Q^T held in VGPRs. The 32x32
+//                   accumulator gives each lane one query column (lane % 32)
+//                   and 16 key rows.
+//   O^T = V^T . P^T A = V^T via transposing reads, B = P^T straight from the
+//                   S^T accumulator after the softmax: the 16 keys a lane
+//                   holds are its B-operand k-slots once the A operand reads
+//                   keys (16ks + 4*(lane/32) + 0..3) and (... + 8 + 0..3).
+// Every lane owns one query row in both products: the softmax needs one
+// cross-half (lane ^ 32) exchange per block for the max, and the rescale of O
 // is lane-local.
 //
 // Layouts (template parameter LAYOUT):
-//   kLayoutQuery: 4 waves x 32 query rows share each 64-key K/V tile staged
-//                 in double-buffered LDS (prefill, Sq > 32).
+//   kLayoutQuery: 4 waves x 32 query rows share each 64-key K/V tile in
+//                 double-buffered LDS (prefill).
 //   kLayoutKey:   4 waves each stream their own 32-key blocks of the same 32
 //                 query rows (decode); the four partial softmax states are
 //                 combined through LDS before the epilogue.
@@ -46,6 +56,7 @@ typedef uint32_t u32;
 typedef uint16_t u16;
 typedef u32 u32x2 __attribute__((ext_vector_type(2)));
 typedef u32 u32x4 __attribute__((ext_vector_type(4)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -53,9 +64,15 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
+#define FGW_LDS(T, p) ((__attribute__((address_space(3))) T*)(p))
+
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kNegBig = -1.0e30f;  // running-max floor and empty-split LSE
 constexpr int kNumXcd = 8;
+constexpr int kLdsBudget = 160 * 1024;
+
+// Source of every masked 16-byte chunk: read-only zeros in device memory.
+static __device__ __attribute__((aligned(64))) const u32 kZeroChunk[16] = {0};
 
 template <bool BF16>
 struct Elem;
@@ -88,11 +105,12 @@ struct Elem<false> {
 // Quotient of a position by the page size (Granlund & Montgomery 1994,
 // "Division by invariant integers using multiplication", fig. 4.1):
 // shift = ceil(log2 page), magic = floor(2^32 (2^shift - page) / page) + 1.
-// shift == 0 encodes page == 1.
+// shift == 0 encodes page == 1. Branch-free: both forms are computed and one
+// is selected.
 __device__ __forceinline__ u32 div_page(u32 n, u32 magic, u32 shift) {
-  if (shift == 0) return n;
   const u32 t = __umulhi(magic, n);
-  return (t + ((n - t) >> 1)) >> (shift - 1);
+  const u32 q = (t + ((n - t) >> 1)) >> ((shift - 1u) & 31u);
+  return shift ? q : n;
 }
 
 // Pool row of logical position `pos` of one request:
@@ -115,18 +133,19 @@ __device__ __forceinline__ int xcd_remap(int bid, int grid) {
   return xcd < r ? xcd * (q + 1) + local : r * (q + 1) + (xcd - r) * q + local;
 }
 
-// 4-key group order inside a 16-key group of the V^T tile: 0,2,1,3.
-__device__ __forceinline__ constexpr int swap12(int x) { return ((x & 1) << 1) | ((x >> 1) & 1); }
-
 template <int A, int B>
 struct CMax {
   static constexpr int value = A > B ? A : B;
+};
+template <int A, int B>
+struct CMin {
+  static constexpr int value = A < B ? A : B;
 };
 
 template <bool BF16_, int DPAD_, int LAYOUT_>
 struct Cfg {
   static constexpr bool BF16 = BF16_;
-  static constexpr int DPAD = DPAD_;  // head dim rounded up to 32
+  static constexpr int DPAD = DPAD_;  // head dim padded to a power of two >= 32
   static constexpr int LAYOUT = LAYOUT_;
   static constexpr int NWQ = LAYOUT == kLayoutQuery ? 4 : 1;  // waves along queries
   static constexpr int NWK = LAYOUT == kLayoutQuery ? 1 : 4;  // waves along keys
@@ -140,33 +159,27 @@ struct Cfg {
   static constexpr int DT = DPAD / 32;  // O^T row tiles
   static constexpr int ST = BN / 32;    // S^T tiles per block
   static constexpr int KS = BN / 16;    // PV k-steps
-  static constexpr int KSTRIDE = DPAD + 8;  // K tile row stride (elements)
-  static constexpr int VSTRIDE = BN + 8;    // V^T tile row stride (elements)
-  static constexpr int K_ELEMS = BN * KSTRIDE;
-  static constexpr int V_ELEMS = DPAD * VSTRIDE;
-  static constexpr int NBUF = NWK == 1 ? 2 : 1;
-  static constexpr int GROUP_ELEMS = NBUF * (K_ELEMS + V_ELEMS);
-  static constexpr int TILE_BYTES = NWK * GROUP_ELEMS * 2;
+  static constexpr int CPR = DPAD / 8;  // 16-byte chunks per LDS row
+  static constexpr int ROW_BYTES = DPAD * 2;
+  static constexpr int TILE_BYTES = BN * ROW_BYTES;  // one K or V tile
+  static constexpr int STAGE_BYTES = 2 * TILE_BYTES;
+  static constexpr int NBUF = NWK * 2 * STAGE_BYTES <= 128 * 1024 ? 2 : 1;
+  static constexpr int GROUP_BYTES = NBUF * STAGE_BYTES;
+  static constexpr int TILES_BYTES = NWK * GROUP_BYTES;
   static constexpr int OSTRIDE = DPAD + 4;  // combine buffer row stride (floats)
   static constexpr int COMB_BYTES =
       NWK > 1 ? (2 * NWK * ROWS_WAVE + NWK * ROWS_WAVE * OSTRIDE) * 4 : 0;
-  static constexpr int LDS_BYTES = CMax<TILE_BYTES, COMB_BYTES>::value;
-  // Loader: the 64 * NWQ threads of a key group fill its tiles.
-  static constexpr int LT = 64 * NWQ;
-  static constexpr int CPR = DPAD / 8;          // 16-byte chunks per key row
-  static constexpr int K_CHUNKS = BN * CPR;     // K: one 16-byte chunk per task
-  static constexpr int K_PER_T = (K_CHUNKS + LT - 1) / LT;
-  static constexpr int V_SUBS = (BN / 4) * CPR; // V: 4 keys x 8 dims per task
-  static constexpr int V_PER_T = (V_SUBS + LT - 1) / LT;
+  static constexpr int LDS_BYTES = CMax<TILES_BYTES, COMB_BYTES>::value;
+  // DMA: one wave instruction fills 1 KB (64 lanes x 16 bytes) of a tile.
+  static constexpr int INSTR = TILE_BYTES / 1024;
+  static constexpr int INSTR_PER_WAVE = INSTR / NWQ;
+  // Chunk swizzles: row r keeps chunk c at slot c ^ x(r).
+  static constexpr int KSW = CMin<8, CPR / 2>::value;  // K: x = 2 * (r % KSW)
+  static constexpr int VSW = CPR / 4;                  // V: x = 4 * (r % VSW)
   static_assert(NWQ == 1 || NWK == 1, "tiles are shared by all waves or by none");
-  static_assert(DPAD % 32 == 0 && DPAD >= 32 && DPAD <= 256, "head dim tile");
-  static_assert(LDS_BYTES <= 160 * 1024, "LDS budget of one CU");
-};
-
-template <class C>
-struct KVFetch {
-  u32x4 k[C::K_PER_T];
-  u32x4 v[C::V_PER_T][4];
+  static_assert((DPAD & (DPAD - 1)) == 0 && DPAD >= 32 && DPAD <= 256, "head dim tile");
+  static_assert(TILE_BYTES % 1024 == 0 && INSTR % NWQ == 0, "DMA granularity");
+  static_assert(LDS_BYTES <= kLdsBudget, "LDS budget of one CU");
 };
 
 // Synchronise the waves that share one key group's tiles.
@@ -181,106 +194,92 @@ __device__ __forceinline__ void group_sync() {
   }
 }
 
-// Global -> registers: the K and V rows of keys [pos0, pos0 + BN) of (b, h).
-// Keys at or beyond `len`, dims at or beyond `dim` and rows whose page id is
-// outside the pool are zero; nothing outside the live cache is read, so NaN
-// in unused pool rows cannot reach the products (cube_general.py:97-109).
+// Wait for this wave's outstanding DMA loads (vmcnt = 0; lgkm and exp untouched).
+__device__ __forceinline__ void wait_dma() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Issue the DMA loads of keys [pos0, pos0 + BN) of (b, h) into one stage
+// (K tile at kt, V tile at vt). Wave `wq` of the key group issues the
+// instructions i = q * NWQ + wq. Slot s = 64 i + lane holds row s / CPR,
+// position s % CPR, i.e. chunk (s % CPR) ^ x(row) of that key row.
+// `id0` is the page id of the page holding pos0 (read ahead by the caller).
 template <class C>
-__device__ __forceinline__ void fetch_block(KVFetch<C>& f, const FwdParams& p,
-                                            const int32_t* table_b, int h, int pos0, int len,
-                                            int lt) {
-  const int64_t row_bytes = (int64_t)p.heads * p.dim * 2;
-  const char* kb = static_cast<const char*>(p.k) + (int64_t)h * p.dim * 2;
-  const char* vb = static_cast<const char*>(p.v) + (int64_t)h * p.dim * 2;
+__device__ __forceinline__ void issue_block(const FwdParams& p, const int32_t* table_b,
+                                            const char* kb, const char* vb, int64_t row_bytes,
+                                            int pos0, int32_t id0, int len, unsigned char* kt,
+                                            unsigned char* vt, int wq, int lane) {
   const u32 page = (u32)p.page_size;
   const u32 pg0 = div_page((u32)pos0, p.page_magic, p.page_shift);
   const u32 off0 = (u32)pos0 - pg0 * page;
-  const bool one_page = off0 + C::BN <= page;
-  const int64_t row0 = one_page ? (int64_t)table_b[pg0] * page + off0 : 0;
-
+  const int64_t row0 = (int64_t)id0 * page + off0;
+  const bool fast = off0 + C::BN <= page && pos0 + C::BN <= len && row0 >= 0 &&
+                    row0 + C::BN <= p.pool_rows;
+  const char* zero = reinterpret_cast<const char*>(kZeroChunk);
+  int64_t rows[C::INSTR_PER_WAVE];
+  if (fast) {
 #pragma unroll
-  for (int r = 0; r < C::K_PER_T; ++r) {
-    const int c = lt + C::LT * r;
-    const int j = c / C::CPR, dc = c % C::CPR;
-    u32x4 val = {0u, 0u, 0u, 0u};
-    const int pos = pos0 + j;
-    if ((C::K_CHUNKS % C::LT == 0 || c < C::K_CHUNKS) && pos < len && dc * 8 < p.dim) {
-      int64_t row;
-      if (one_page) {
-        row = row0 + j;
-        row = (row >= 0 && row < p.pool_rows) ? row : -1;
-      } else {
-        row = phys_row(table_b, (u32)pos, page, p.page_magic, p.page_shift, p.pool_rows);
-      }
-      if (row >= 0) val = load16(kb + row * row_bytes + dc * 16);
+    for (int q = 0; q < C::INSTR_PER_WAVE; ++q)
+      rows[q] = row0 + (64 * (q * C::NWQ + wq) + lane) / C::CPR;
+  } else {
+    int32_t ids[C::INSTR_PER_WAVE];
+#pragma unroll
+    for (int q = 0; q < C::INSTR_PER_WAVE; ++q) {
+      const int pos = pos0 + (64 * (q * C::NWQ + wq) + lane) / C::CPR;
+      const u32 pg = pos < len ? div_page((u32)pos, p.page_magic, p.page_shift) : 0u;
+      ids[q] = table_b[pg];
     }
-    f.k[r] = val;
+#pragma unroll
+    for (int q = 0; q < C::INSTR_PER_WAVE; ++q) {
+      const int pos = pos0 + (64 * (q * C::NWQ + wq) + lane) / C::CPR;
+      const u32 pg = div_page((u32)pos, p.page_magic, p.page_shift);
+      const int64_t row = (int64_t)ids[q] * page + ((u32)pos - pg * page);
+      rows[q] = (pos < len && row >= 0 && row < p.pool_rows) ? row : -1;
+    }
   }
 #pragma unroll
-  for (int r = 0; r < C::V_PER_T; ++r) {
-    const int sidx = lt + C::LT * r;
-    const int jg = sidx / C::CPR, dc = sidx % C::CPR;
-    const bool task = (C::V_SUBS % C::LT == 0 || sidx < C::V_SUBS) && dc * 8 < p.dim;
-#pragma unroll
-    for (int x = 0; x < 4; ++x) {
-      u32x4 val = {0u, 0u, 0u, 0u};
-      const int pos = pos0 + 4 * jg + x;
-      if (task && pos < len) {
-        int64_t row;
-        if (one_page) {
-          row = row0 + 4 * jg + x;
-          row = (row >= 0 && row < p.pool_rows) ? row : -1;
-        } else {
-          row = phys_row(table_b, (u32)pos, page, p.page_magic, p.page_shift, p.pool_rows);
-        }
-        if (row >= 0) val = load16(vb + row * row_bytes + dc * 16);
-      }
-      f.v[r][x] = val;
-    }
+  for (int q = 0; q < C::INSTR_PER_WAVE; ++q) {
+    const int i = q * C::NWQ + wq;
+    const int s = 64 * i + lane;
+    const int r = s / C::CPR, pos_in_row = s % C::CPR;
+    const int ck = pos_in_row ^ (2 * (r % C::KSW));
+    const int cv = pos_in_row ^ (4 * (r % C::VSW));
+    const bool live = rows[q] >= 0;
+    const char* ks = live && ck * 8 < p.dim ? kb + rows[q] * row_bytes + ck * 16 : zero;
+    const char* vs = live && cv * 8 < p.dim ? vb + rows[q] * row_bytes + cv * 16 : zero;
+    __builtin_amdgcn_global_load_lds(ks, FGW_LDS(void, kt + 1024 * i), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(vs, FGW_LDS(void, vt + 1024 * i), 16, 0, 0);
   }
 }
 
-// Registers -> LDS. K rows as they are; V transposed to V^T[d][key] with
-// the 4-key group swap, via byte permutes (4 keys x 8 dims per task).
+// Per-lane LDS byte offsets of the MFMA A operands (see issue_block):
+//   K: row il (+32 t), chunk 2 kk + hh  -> il*ROW + 16 hh + 32 (kk ^ (il % KSW))
+//   V: transposing read of group g = lane / 16, lane j = lane % 16:
+//      row (16 ks + 8 half) + 4 (g / 2) + j / 4, dims 32 dt + 16 (g % 2) + 4 (j % 4)
+//      -> vbase + (16 ks + 8 half) * ROW + 64 (dt ^ vy), vy = (4 (g / 2) + j / 4) % VSW
 template <class C>
-__device__ __forceinline__ void store_block(const KVFetch<C>& f, u16* ks, u16* vts, int lt) {
-#pragma unroll
-  for (int r = 0; r < C::K_PER_T; ++r) {
-    const int c = lt + C::LT * r;
-    if (C::K_CHUNKS % C::LT == 0 || c < C::K_CHUNKS) {
-      const int j = c / C::CPR, dc = c % C::CPR;
-      *reinterpret_cast<u32x4*>(ks + j * C::KSTRIDE + dc * 8) = f.k[r];
-    }
+struct Lanes {
+  int k_base;  // + t * 32 * ROW_BYTES + 32 * (kk ^ ky)
+  int ky;
+  int v_base;  // + (16 ks + 8 half) * ROW_BYTES + 64 * (dt ^ vy)
+  int vy;
+  __device__ __forceinline__ explicit Lanes(int lane) {
+    const int il = lane & 31, hh = lane >> 5;
+    ky = il % C::KSW;
+    k_base = il * C::ROW_BYTES + 16 * hh;
+    const int g = lane >> 4, j = lane & 15;
+    const int vrow = 4 * (g >> 1) + (j >> 2);
+    vy = vrow % C::VSW;
+    v_base = vrow * C::ROW_BYTES + 32 * (g & 1) + 8 * (j & 3);
   }
-#pragma unroll
-  for (int r = 0; r < C::V_PER_T; ++r) {
-    const int sidx = lt + C::LT * r;
-    if (C::V_SUBS % C::LT == 0 || sidx < C::V_SUBS) {
-      const int jg = sidx / C::CPR, dc = sidx % C::CPR;
-      const int col = 16 * (jg >> 2) + 4 * swap12(jg & 3);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-#pragma unroll
-        for (int xx = 0; xx < 2; ++xx) {
-          const u32 sel = xx ? 0x07060302u : 0x05040100u;
-          u32x2 w;
-          w.x = __builtin_amdgcn_perm(f.v[r][1][e], f.v[r][0][e], sel);
-          w.y = __builtin_amdgcn_perm(f.v[r][3][e], f.v[r][2][e], sel);
-          *reinterpret_cast<u32x2*>(vts + (8 * dc + 2 * e + xx) * C::VSTRIDE + col) = w;
-        }
-      }
-    }
-  }
-}
+};
 
 // One BN-key block for one wave: S^T = K Q^T, online softmax, O^T += V^T P^T.
 template <class C>
-__device__ __forceinline__ void compute_block(const u16* ks, const u16* vts,
+__device__ __forceinline__ void compute_block(const unsigned char* kt, const unsigned char* vt,
+                                              const Lanes<C>& ln,
                                               const u32x4 (&qf)[C::QG][C::KK],
                                               f32x16 (&o)[C::QG][C::DT], float (&m)[C::QG],
                                               float (&l)[C::QG], const int (&vis)[C::QG], int pos0,
-                                              bool need_mask, float scale_log2, int kk_live,
-                                              int il, int hh) {
+                                              bool need_mask, float scale_log2, int hh) {
   using E = Elem<C::BF16>;
   f32x16 s[C::QG][C::ST];
 #pragma unroll
@@ -292,16 +291,15 @@ __device__ __forceinline__ void compute_block(const u16* ks, const u16* vts,
 
 #pragma unroll
   for (int kk = 0; kk < C::KK; ++kk) {
-    if (kk < kk_live) {
-      u32x4 a[C::ST];
+    const unsigned char* ka = kt + ln.k_base + 32 * (kk ^ ln.ky);
+    u32x4 a[C::ST];
 #pragma unroll
-      for (int t = 0; t < C::ST; ++t)
-        a[t] = *reinterpret_cast<const u32x4*>(ks + (32 * t + il) * C::KSTRIDE + 16 * kk + 8 * hh);
+    for (int t = 0; t < C::ST; ++t)
+      a[t] = *reinterpret_cast<const u32x4*>(ka + t * 32 * C::ROW_BYTES);
 #pragma unroll
-      for (int g = 0; g < C::QG; ++g)
+    for (int g = 0; g < C::QG; ++g)
 #pragma unroll
-        for (int t = 0; t < C::ST; ++t) s[g][t] = E::mma(a[t], qf[g][kk], s[g][t]);
-    }
+      for (int t = 0; t < C::ST; ++t) s[g][t] = E::mma(a[t], qf[g][kk], s[g][t]);
   }
 
   u32x4 pf[C::QG][C::KS];
@@ -353,14 +351,20 @@ __device__ __forceinline__ void compute_block(const u16* ks, const u16* vts,
   }
 
 #pragma unroll
-  for (int k2 = 0; k2 < C::KS; ++k2)
+  for (int dt = 0; dt < C::DT; ++dt) {
+    const unsigned char* va = vt + ln.v_base + 64 * (dt ^ ln.vy);
 #pragma unroll
-    for (int dt = 0; dt < C::DT; ++dt) {
-      const u32x4 a =
-          *reinterpret_cast<const u32x4*>(vts + (32 * dt + il) * C::VSTRIDE + 16 * k2 + 8 * hh);
+    for (int k2 = 0; k2 < C::KS; ++k2) {
+      const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          FGW_LDS(i16x4, va + (16 * k2) * C::ROW_BYTES));
+      const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          FGW_LDS(i16x4, va + (16 * k2 + 8) * C::ROW_BYTES));
+      const u32x2 lo2 = __builtin_bit_cast(u32x2, lo), hi2 = __builtin_bit_cast(u32x2, hi);
+      const u32x4 a = {lo2.x, lo2.y, hi2.x, hi2.y};
 #pragma unroll
       for (int g = 0; g < C::QG; ++g) o[g][dt] = E::mma(a, pf[g][k2], o[g][dt]);
     }
+  }
 }
 
 template <class C>
@@ -384,9 +388,18 @@ __device__ __forceinline__ float lse_of(float m_log2, float total) {
   return total > 0.0f ? (m_log2 + log2f(total)) * kLn2 : kNegBig;
 }
 
+// Page id of the page holding logical position pos.
+__device__ __forceinline__ int32_t page_id(const FwdParams& p, const int32_t* table_b, int pos) {
+  return table_b[div_page((u32)pos, p.page_magic, p.page_shift)];
+}
+
+// table and lengths come as separate read-only, non-aliasing arguments so
+// that uniform reads of them can use the scalar cache.
 template <class C>
-__global__ __launch_bounds__(C::THREADS) void fwd_kernel(FwdParams p) {
-  __shared__ __attribute__((aligned(16))) unsigned char smem[C::LDS_BYTES];
+__global__ __launch_bounds__(C::THREADS) void fwd_kernel(FwdParams p,
+                                                         const int32_t* __restrict__ table,
+                                                         const int32_t* __restrict__ lengths) {
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[C::LDS_BYTES];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -394,8 +407,9 @@ __global__ __launch_bounds__(C::THREADS) void fwd_kernel(FwdParams p) {
   const int il = lane & 31, hh = lane >> 5;
   const int wq = C::NWQ > 1 ? wave : 0;
   const int wk = C::NWK > 1 ? wave : 0;
-  const int lt = C::NWQ > 1 ? tid : lane;
-  u16* const group_base = reinterpret_cast<u16*>(smem) + wk * C::GROUP_ELEMS;
+  unsigned char* const group_base = smem + wk * C::GROUP_BYTES;
+  const Lanes<C> ln(lane);
+  const int64_t row_bytes = (int64_t)p.heads * p.dim * 2;
 
   const int grid = gridDim.x;
   const int prog = xcd_remap(blockIdx.x, grid);
@@ -403,7 +417,6 @@ __global__ __launch_bounds__(C::THREADS) void fwd_kernel(FwdParams p) {
   const int first = prog * per + (prog < rem ? prog : rem);
   const int count = per + (prog < rem ? 1 : 0);
   const int capacity = p.width * p.page_size;
-  const int kk_live = (p.dim + 15) >> 4;
 
   for (int it = 0; it < count; ++it) {
     int w = first + it;
@@ -413,9 +426,11 @@ __global__ __launch_bounds__(C::THREADS) void fwd_kernel(FwdParams p) {
     w /= p.q_tiles;
     const int h = w % p.heads;
     const int b = w / p.heads;
-    const int32_t* table_b = p.table + (int64_t)b * p.width;
+    const int32_t* table_b = table + (int64_t)b * p.width;
+    const char* kb = static_cast<const char*>(p.k) + (int64_t)h * p.dim * 2;
+    const char* vb = static_cast<const char*>(p.v) + (int64_t)h * p.dim * 2;
 
-    int len = p.lengths[b];
+    int len = lengths[b];
     len = len < 0 ? 0 : (len > capacity ? capacity : len);
     const int q0 = qt * C::ROWS_TILE;
     const int tile_last = (q0 + C::ROWS_TILE < p.sq ? q0 + C::ROWS_TILE : p.sq) - 1;
@@ -461,27 +476,36 @@ __global__ __launch_bounds__(C::THREADS) void fwd_kernel(FwdParams p) {
         for (int v = 0; v < 16; ++v) o[g][dt][v] = 0.0f;
     }
 
+    // Block n of this key group starts at key (blk_begin + wk + NWK n) * BN.
+    // Page ids are read one block ahead of their DMA issue.
+    constexpr int kStep = C::NWK * C::BN;
+    const int first_pos = (blk_begin + wk) * C::BN;
+    int32_t next_id = my_n > 1 ? page_id(p, table_b, first_pos + kStep) : 0;
     __syncthreads();  // LDS of the previous work item is no longer read
-    KVFetch<C> f;
     if (my_n > 0) {
-      fetch_block<C>(f, p, table_b, h, (blk_begin + wk) * C::BN, len, lt);
-      store_block<C>(f, group_base, group_base + C::K_ELEMS, lt);
-      group_sync<C>();
+      issue_block<C>(p, table_b, kb, vb, row_bytes, first_pos, page_id(p, table_b, first_pos),
+                     len, group_base, group_base + C::TILE_BYTES, wq, lane);
     }
     for (int n = 0; n < my_n; ++n) {
-      const int pos0 = (blk_begin + wk + C::NWK * n) * C::BN;
-      const bool more = n + 1 < my_n;
-      if (more) fetch_block<C>(f, p, table_b, h, pos0 + C::NWK * C::BN, len, lt);
-      const u16* ks = group_base + (n % C::NBUF) * (C::K_ELEMS + C::V_ELEMS);
-      if (wave_active && pos0 < wmax) {
-        compute_block<C>(ks, ks + C::K_ELEMS, qf, o, m, l, vis, pos0, pos0 + C::BN > wmin,
-                         p.scale_log2, kk_live, il, hh);
+      const int pos0 = first_pos + kStep * n;
+      unsigned char* stage = group_base + (n % C::NBUF) * C::STAGE_BYTES;
+      wait_dma();
+      group_sync<C>();  // stage n is in LDS; everyone is done with stage n - 1
+      const int32_t id1 = next_id;
+      if (n + 2 < my_n) next_id = page_id(p, table_b, pos0 + 2 * kStep);
+      if (n + 1 < my_n && C::NBUF == 2) {
+        unsigned char* next = group_base + ((n + 1) % C::NBUF) * C::STAGE_BYTES;
+        issue_block<C>(p, table_b, kb, vb, row_bytes, pos0 + kStep, id1, len, next,
+                       next + C::TILE_BYTES, wq, lane);
       }
-      if (more) {
-        if constexpr (C::NBUF == 1) group_sync<C>();
-        u16* nk = group_base + ((n + 1) % C::NBUF) * (C::K_ELEMS + C::V_ELEMS);
-        store_block<C>(f, nk, nk + C::K_ELEMS, lt);
-        group_sync<C>();
+      if (wave_active && pos0 < wmax) {
+        compute_block<C>(stage, stage + C::TILE_BYTES, ln, qf, o, m, l, vis, pos0,
+                         pos0 + C::BN > wmin, p.scale_log2, hh);
+      }
+      if (n + 1 < my_n && C::NBUF == 1) {
+        group_sync<C>();  // single stage: refill only after every wave has read it
+        issue_block<C>(p, table_b, kb, vb, row_bytes, pos0 + kStep, id1, len, stage,
+                       stage + C::TILE_BYTES, wq, lane);
       }
     }
 
@@ -564,13 +588,9 @@ __global__ __launch_bounds__(C::THREADS) void fwd_kernel(FwdParams p) {
 template <bool BF16, int DPAD, int LAYOUT>
 hipError_t launch_fwd(const FwdParams& p, int grid, hipStream_t stream) {
   using C = Cfg<BF16, DPAD, LAYOUT>;
-  fwd_kernel<C><<<dim3(grid), dim3(C::THREADS), 0, stream>>>(p);
+  fwd_kernel<C><<<dim3(grid), dim3(C::THREADS), 0, stream>>>(p, p.table, p.lengths);
   return hipGetLastError();
 }
-
-}  // namespace fgw_mha
-
-namespace fgw_mha {
 
 // Resident workgroups per CU of one instantiation (0 if the query fails).
 template <bool BF16, int DPAD, int LAYOUT>

@@ -14,8 +14,13 @@ struct FwdEntry {
   OccupancyFn occupancy;
 };
 
-// Head-dim tiles with a compiled kernel: 32, 64, ..., 256.
-inline int dim_tile(int dim) { return (dim + 31) / 32 * 32; }
+// Head-dim tiles with a compiled kernel: 32, 64, 128, 256 (D padded to a
+// power of two, cube_general.py:31).
+inline int dim_tile(int dim) {
+  int t = 32;
+  while (t < dim) t *= 2;
+  return t;
+}
 
 FwdEntry fwd_entry(bool bf16, int dpad, int layout);
 hipError_t launch_merge(bool bf16, const MergeParams& p, hipStream_t stream);
@@ -24,8 +29,8 @@ hipError_t launch_gather(const GatherParams& p, hipStream_t stream);
 }  // namespace fgw_mha
 
 // Explicit instantiation lists, expanded once per translation unit.
-#define FGW_MHA_FOR_DPAD_LO(X, BF) X(BF, 32) X(BF, 64) X(BF, 96) X(BF, 128)
-#define FGW_MHA_FOR_DPAD_HI(X, BF) X(BF, 160) X(BF, 192) X(BF, 224) X(BF, 256)
+#define FGW_MHA_FOR_DPAD_LO(X, BF) X(BF, 32) X(BF, 64)
+#define FGW_MHA_FOR_DPAD_HI(X, BF) X(BF, 128) X(BF, 256)
 #define FGW_MHA_INSTANTIATE(BF, DP)                                                         \
   template hipError_t launch_fwd<BF, DP, kLayoutQuery>(const FwdParams&, int, hipStream_t); \
   template hipError_t launch_fwd<BF, DP, kLayoutKey>(const FwdParams&, int, hipStream_t);   \
