@@ -68,6 +68,7 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kNegBig = -1.0e30f;  // running-max floor and empty-split LSE
+constexpr float kRescaleSlack = 8.0f;  // log2 headroom of p before O/l are rescaled
 constexpr int kNumXcd = 8;
 constexpr int kLdsBudget = 160 * 1024;
 
@@ -150,10 +151,9 @@ struct Cfg {
   static constexpr int NWQ = LAYOUT == kLayoutQuery ? 4 : 1;  // waves along queries
   static constexpr int NWK = LAYOUT == kLayoutQuery ? 1 : 4;  // waves along keys
   static constexpr int BN = LAYOUT == kLayoutQuery ? 64 : 32; // keys per block
-  static constexpr int QG = 1;                                // 32-row groups per wave
   static constexpr int WAVES = NWQ * NWK;
   static constexpr int THREADS = 64 * WAVES;
-  static constexpr int ROWS_WAVE = 32 * QG;
+  static constexpr int ROWS_WAVE = 32;
   static constexpr int ROWS_TILE = ROWS_WAVE * NWQ;
   static constexpr int KK = DPAD / 16;  // QK k-steps
   static constexpr int DT = DPAD / 32;  // O^T row tiles
@@ -173,12 +173,15 @@ struct Cfg {
   // DMA: one wave instruction fills 1 KB (64 lanes x 16 bytes) of a tile.
   static constexpr int INSTR = TILE_BYTES / 1024;
   static constexpr int INSTR_PER_WAVE = INSTR / NWQ;
-  // Chunk swizzles: row r keeps chunk c at slot c ^ x(r).
-  static constexpr int KSW = CMin<8, CPR / 2>::value;  // K: x = 2 * (r % KSW)
-  static constexpr int VSW = CPR / 4;                  // V: x = 4 * (r % VSW)
+  // Chunk swizzles: row r keeps chunk c at slot c ^ x(r). K rows are read 16
+  // rows at a time at one chunk column, so x spreads 16 rows over 16 slots;
+  // V rows are read 4 rows x 64 bytes at a time, so x moves 64-byte spans.
+  static constexpr int KSW = CMin<16, CPR>::value;  // K: x = r % KSW
+  static constexpr int VSW = CPR / 4;               // V: x = 4 * (r % VSW)
+  static constexpr int RPI = 64 / CPR;              // key rows per DMA instruction
   static_assert(NWQ == 1 || NWK == 1, "tiles are shared by all waves or by none");
   static_assert((DPAD & (DPAD - 1)) == 0 && DPAD >= 32 && DPAD <= 256, "head dim tile");
-  static_assert(TILE_BYTES % 1024 == 0 && INSTR % NWQ == 0, "DMA granularity");
+  static_assert(TILE_BYTES % 1024 == 0 && INSTR % NWQ == 0 && 64 % CPR == 0, "DMA granularity");
   static_assert(LDS_BYTES <= kLdsBudget, "LDS budget of one CU");
 };
 
@@ -197,74 +200,111 @@ __device__ __forceinline__ void group_sync() {
 // Wait for this wave's outstanding DMA loads (vmcnt = 0; lgkm and exp untouched).
 __device__ __forceinline__ void wait_dma() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
-// Issue the DMA loads of keys [pos0, pos0 + BN) of (b, h) into one stage
-// (K tile at kt, V tile at vt). Wave `wq` of the key group issues the
-// instructions i = q * NWQ + wq. Slot s = 64 i + lane holds row s / CPR,
-// position s % CPR, i.e. chunk (s % CPR) ^ x(row) of that key row.
-// `id0` is the page id of the page holding pos0 (read ahead by the caller).
+// Per-lane DMA offsets. Instruction i of a stage fills slots 64 i + lane:
+// key row RPI i + lr (lr = lane / CPR), position pos = lane % CPR, which
+// holds chunk pos ^ x(row). Because RPI i % KSW is a multiple of RPI and
+// lr < RPI, x(row) = (RPI i % KSW) | lr, so the chunk is (pos ^ lr) ^ c_i with
+// c_i = RPI i % KSW; likewise for V with 4 (row % VSW). Offsets are
+// precomputed per instruction when a wave issues few of them, otherwise
+// derived with one XOR each.
 template <class C>
-__device__ __forceinline__ void issue_block(const FwdParams& p, const int32_t* table_b,
-                                            const char* kb, const char* vb, int64_t row_bytes,
-                                            int pos0, int32_t id0, int len, unsigned char* kt,
-                                            unsigned char* vt, int wq, int lane) {
+struct DmaLanes {
+  static constexpr bool PRE = C::INSTR_PER_WAVE <= 4;
+  static constexpr int NPRE = PRE ? C::INSTR_PER_WAVE : 1;
+  u32 row_off;  // lr * row_bytes
+  u32 kx, vx;   // 16 (pos ^ lr), 16 (pos ^ 4 (lr % VSW)), pre-XOR chunk bytes
+  u32 koff[NPRE];
+  u32 voff[NPRE];
+  __device__ __forceinline__ DmaLanes(int lane, int wq, int64_t row_bytes) {
+    const int lr = lane / C::CPR, pos = lane % C::CPR;
+    row_off = (u32)(lr * row_bytes);
+    kx = 16u * (u32)(pos ^ (lr % C::KSW));
+    vx = 16u * (u32)(pos ^ (4 * (lr % C::VSW)));
+#pragma unroll
+    for (int q = 0; q < NPRE; ++q) {
+      koff[q] = k(q, wq);
+      voff[q] = v(q, wq);
+    }
+  }
+  __device__ __forceinline__ u32 k(int q, int wq) const {
+    const int i = q * C::NWQ + wq;
+    return row_off + (kx ^ (16u * (u32)((C::RPI * i) % C::KSW)));
+  }
+  __device__ __forceinline__ u32 v(int q, int wq) const {
+    const int i = q * C::NWQ + wq;
+    return row_off + (vx ^ (64u * (u32)((C::RPI * i) % C::VSW)));
+  }
+  __device__ __forceinline__ u32 kq(int q, int wq) const { return PRE ? koff[PRE ? q : 0] : k(q, wq); }
+  __device__ __forceinline__ u32 vq(int q, int wq) const { return PRE ? voff[PRE ? q : 0] : v(q, wq); }
+};
+
+// Issue the DMA loads of the K (IS_V false) or V tile of keys
+// [pos0, pos0 + BN) of (b, h) into LDS at `dst`. Wave `wq` of the key group
+// issues the instructions i = q * NWQ + wq. `id0` is the page id of the page
+// holding pos0 (read ahead by the caller). A block inside one page, below
+// len, with no padded dims takes the fast path: uniform row base + per-lane
+// offset. Otherwise every key is resolved through the table and masked
+// chunks read the zero chunk.
+template <class C, bool IS_V>
+__device__ __forceinline__ void issue_tile(const FwdParams& p, const DmaLanes<C>& dl,
+                                           const int32_t* table_b, const char* base,
+                                           int64_t row_bytes, int pos0, int32_t id0, int len,
+                                           unsigned char* dst, int wq, int lane) {
   const u32 page = (u32)p.page_size;
   const u32 pg0 = div_page((u32)pos0, p.page_magic, p.page_shift);
   const u32 off0 = (u32)pos0 - pg0 * page;
   const int64_t row0 = (int64_t)id0 * page + off0;
   const bool fast = off0 + C::BN <= page && pos0 + C::BN <= len && row0 >= 0 &&
-                    row0 + C::BN <= p.pool_rows;
-  const char* zero = reinterpret_cast<const char*>(kZeroChunk);
-  int64_t rows[C::INSTR_PER_WAVE];
+                    row0 + C::BN <= p.pool_rows && p.dim == C::DPAD;
   if (fast) {
 #pragma unroll
-    for (int q = 0; q < C::INSTR_PER_WAVE; ++q)
-      rows[q] = row0 + (64 * (q * C::NWQ + wq) + lane) / C::CPR;
-  } else {
-    int32_t ids[C::INSTR_PER_WAVE];
-#pragma unroll
     for (int q = 0; q < C::INSTR_PER_WAVE; ++q) {
-      const int pos = pos0 + (64 * (q * C::NWQ + wq) + lane) / C::CPR;
-      const u32 pg = pos < len ? div_page((u32)pos, p.page_magic, p.page_shift) : 0u;
-      ids[q] = table_b[pg];
+      const int i = q * C::NWQ + wq;
+      const int64_t rb = (row0 + C::RPI * i) * row_bytes;
+      const u32 off = IS_V ? dl.vq(q, wq) : dl.kq(q, wq);
+      __builtin_amdgcn_global_load_lds(base + rb + off, FGW_LDS(void, dst + 1024 * i), 16, 0, 0);
     }
+    return;
+  }
+  const char* zero = reinterpret_cast<const char*>(kZeroChunk);
+  int32_t ids[C::INSTR_PER_WAVE];
 #pragma unroll
-    for (int q = 0; q < C::INSTR_PER_WAVE; ++q) {
-      const int pos = pos0 + (64 * (q * C::NWQ + wq) + lane) / C::CPR;
-      const u32 pg = div_page((u32)pos, p.page_magic, p.page_shift);
-      const int64_t row = (int64_t)ids[q] * page + ((u32)pos - pg * page);
-      rows[q] = (pos < len && row >= 0 && row < p.pool_rows) ? row : -1;
-    }
+  for (int q = 0; q < C::INSTR_PER_WAVE; ++q) {
+    const int pos = pos0 + C::RPI * (q * C::NWQ + wq) + lane / C::CPR;
+    const u32 pg = pos < len ? div_page((u32)pos, p.page_magic, p.page_shift) : 0u;
+    ids[q] = table_b[pg];
   }
 #pragma unroll
   for (int q = 0; q < C::INSTR_PER_WAVE; ++q) {
     const int i = q * C::NWQ + wq;
-    const int s = 64 * i + lane;
-    const int r = s / C::CPR, pos_in_row = s % C::CPR;
-    const int ck = pos_in_row ^ (2 * (r % C::KSW));
-    const int cv = pos_in_row ^ (4 * (r % C::VSW));
-    const bool live = rows[q] >= 0;
-    const char* ks = live && ck * 8 < p.dim ? kb + rows[q] * row_bytes + ck * 16 : zero;
-    const char* vs = live && cv * 8 < p.dim ? vb + rows[q] * row_bytes + cv * 16 : zero;
-    __builtin_amdgcn_global_load_lds(ks, FGW_LDS(void, kt + 1024 * i), 16, 0, 0);
-    __builtin_amdgcn_global_load_lds(vs, FGW_LDS(void, vt + 1024 * i), 16, 0, 0);
+    const int r = C::RPI * i + lane / C::CPR, pos_in_row = lane % C::CPR;
+    const int pos = pos0 + r;
+    const u32 pg = div_page((u32)pos, p.page_magic, p.page_shift);
+    const int64_t row = (int64_t)ids[q] * page + ((u32)pos - pg * page);
+    const bool live = pos < len && row >= 0 && row < p.pool_rows;
+    const int c = IS_V ? pos_in_row ^ (4 * (r % C::VSW)) : pos_in_row ^ (r % C::KSW);
+    const char* src = live && c * 8 < p.dim ? base + row * row_bytes + c * 16 : zero;
+    __builtin_amdgcn_global_load_lds(src, FGW_LDS(void, dst + 1024 * i), 16, 0, 0);
   }
 }
 
 // Per-lane LDS byte offsets of the MFMA A operands (see issue_block):
-//   K: row il (+32 t), chunk 2 kk + hh  -> il*ROW + 16 hh + 32 (kk ^ (il % KSW))
+//   K: row il (+32 t), chunk 2 kk + hh at slot (2 kk + hh) ^ x, x = il % KSW
+//      -> il*ROW + 16 (hh ^ (x & 1)) + 32 (kk ^ (x >> 1))
 //   V: transposing read of group g = lane / 16, lane j = lane % 16:
 //      row (16 ks + 8 half) + 4 (g / 2) + j / 4, dims 32 dt + 16 (g % 2) + 4 (j % 4)
 //      -> vbase + (16 ks + 8 half) * ROW + 64 (dt ^ vy), vy = (4 (g / 2) + j / 4) % VSW
 template <class C>
 struct Lanes {
   int k_base;  // + t * 32 * ROW_BYTES + 32 * (kk ^ ky)
-  int ky;
+  int ky;      // (il % KSW) >> 1
   int v_base;  // + (16 ks + 8 half) * ROW_BYTES + 64 * (dt ^ vy)
   int vy;
   __device__ __forceinline__ explicit Lanes(int lane) {
     const int il = lane & 31, hh = lane >> 5;
-    ky = il % C::KSW;
-    k_base = il * C::ROW_BYTES + 16 * hh;
+    const int x = il % C::KSW;
+    ky = x >> 1;
+    k_base = il * C::ROW_BYTES + 16 * (hh ^ (x & 1));
     const int g = lane >> 4, j = lane & 15;
     const int vrow = 4 * (g >> 1) + (j >> 2);
     vy = vrow % C::VSW;
@@ -272,98 +312,130 @@ struct Lanes {
   }
 };
 
-// One BN-key block for one wave: S^T = K Q^T, online softmax, O^T += V^T P^T.
+// A operand of S^T tile t, k-step kk: 8 K elements of key row 32 t + il.
 template <class C>
-__device__ __forceinline__ void compute_block(const unsigned char* kt, const unsigned char* vt,
-                                              const Lanes<C>& ln,
-                                              const u32x4 (&qf)[C::QG][C::KK],
-                                              f32x16 (&o)[C::QG][C::DT], float (&m)[C::QG],
-                                              float (&l)[C::QG], const int (&vis)[C::QG], int pos0,
-                                              bool need_mask, float scale_log2, int hh) {
-  using E = Elem<C::BF16>;
-  f32x16 s[C::QG][C::ST];
-#pragma unroll
-  for (int g = 0; g < C::QG; ++g)
-#pragma unroll
-    for (int t = 0; t < C::ST; ++t)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) s[g][t][v] = 0.0f;
+__device__ __forceinline__ u32x4 read_k(const unsigned char* kt, const Lanes<C>& ln, int t,
+                                        int kk) {
+  return *reinterpret_cast<const u32x4*>(kt + ln.k_base + 32 * (kk ^ ln.ky) +
+                                         t * 32 * C::ROW_BYTES);
+}
 
+// A operand of O^T tile dt, PV k-step k2: V[16 k2 + 4 (lane/32) + {0..3, 8..11}][32 dt + lane%32]
+// from two transposing reads of row-major V.
+template <class C>
+__device__ __forceinline__ u32x4 read_vt(const unsigned char* vt, const Lanes<C>& ln, int dt,
+                                         int k2) {
+  const unsigned char* va = vt + ln.v_base + 64 * (dt ^ ln.vy) + (16 * k2) * C::ROW_BYTES;
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(FGW_LDS(i16x4, va));
+  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(FGW_LDS(i16x4, va + 8 * C::ROW_BYTES));
+  const u32x2 lo2 = __builtin_bit_cast(u32x2, lo), hi2 = __builtin_bit_cast(u32x2, hi);
+  return u32x4{lo2.x, lo2.y, hi2.x, hi2.y};
+}
+
+// S^T tiles of one BN-key block: s[t] = K[32 t .. 32 t + 31] . Q^T, with the
+// K operands read one k-step ahead of the MFMAs that consume them.
+template <class C>
+__device__ __forceinline__ void qk_block(const unsigned char* kt, const Lanes<C>& ln,
+                                         const u32x4 (&qf)[C::KK], f32x16 (&s)[C::ST]) {
+  using E = Elem<C::BF16>;
+#pragma unroll
+  for (int t = 0; t < C::ST; ++t)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) s[t][v] = 0.0f;
+  u32x4 a[2][C::ST];
+#pragma unroll
+  for (int t = 0; t < C::ST; ++t) a[0][t] = read_k<C>(kt, ln, t, 0);
 #pragma unroll
   for (int kk = 0; kk < C::KK; ++kk) {
-    const unsigned char* ka = kt + ln.k_base + 32 * (kk ^ ln.ky);
-    u32x4 a[C::ST];
+    if (kk + 1 < C::KK) {
 #pragma unroll
-    for (int t = 0; t < C::ST; ++t)
-      a[t] = *reinterpret_cast<const u32x4*>(ka + t * 32 * C::ROW_BYTES);
+      for (int t = 0; t < C::ST; ++t) a[(kk + 1) & 1][t] = read_k<C>(kt, ln, t, kk + 1);
+    }
 #pragma unroll
-    for (int g = 0; g < C::QG; ++g)
-#pragma unroll
-      for (int t = 0; t < C::ST; ++t) s[g][t] = E::mma(a[t], qf[g][kk], s[g][t]);
+    for (int t = 0; t < C::ST; ++t) s[t] = E::mma(a[kk & 1][t], qf[kk], s[t]);
   }
+}
 
-  u32x4 pf[C::QG][C::KS];
+// Scores of keys at or beyond the lane's visible count become -inf.
+template <class C>
+__device__ __forceinline__ void mask_block(f32x16 (&s)[C::ST], int pos0, int vis, int hh) {
 #pragma unroll
-  for (int g = 0; g < C::QG; ++g) {
-    if (need_mask) {
+  for (int t = 0; t < C::ST; ++t)
 #pragma unroll
-      for (int t = 0; t < C::ST; ++t)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int key = pos0 + 32 * t + 8 * (v >> 2) + 4 * hh + (v & 3);
-          if (key >= vis[g]) s[g][t][v] = -INFINITY;
-        }
+    for (int v = 0; v < 16; ++v) {
+      const int key = pos0 + 32 * t + 8 * (v >> 2) + 4 * hh + (v & 3);
+      if (key >= vis) s[t][v] = -INFINITY;
     }
-    float mx = -INFINITY;
+}
+
+// Row maximum of the block, in log2 units, over the lane pair (lane, lane ^ 32).
+template <class C>
+__device__ __forceinline__ float row_max(const f32x16 (&s)[C::ST], float scale_log2) {
+  float mx = -INFINITY;
 #pragma unroll
-    for (int t = 0; t < C::ST; ++t)
+  for (int t = 0; t < C::ST; ++t)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[g][t][v]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float mn = fmaxf(m[g], mx * scale_log2);
-    const float alpha = __builtin_amdgcn_exp2f(m[g] - mn);
-    float rs = 0.0f;
+    for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[t][v]);
+  return fmaxf(mx, __shfl_xor(mx, 32)) * scale_log2;
+}
+
+// The exponent reference m moves only when a row maximum of the wave exceeds
+// it by more than kRescaleSlack (log2 units): p stays <= 2^kRescaleSlack and
+// the O/l rescale runs on few blocks. O/l and the LSE do not depend on m.
+template <class C>
+__device__ __forceinline__ void update_ref(float mx, float& m, float& l, f32x16 (&o)[C::DT]) {
+  if (__ballot(mx > m + kRescaleSlack)) {
+    const float mn = fmaxf(m, mx);
+    const float alpha = __builtin_amdgcn_exp2f(m - mn);
+    l *= alpha;
 #pragma unroll
-    for (int t = 0; t < C::ST; ++t)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[g][t][v], scale_log2, -mn));
-        s[g][t][v] = e;
-        rs += e;
-      }
-    l[g] = l[g] * alpha + rs;
-    m[g] = mn;
-    if (__ballot(alpha != 1.0f)) {
-#pragma unroll
-      for (int dt = 0; dt < C::DT; ++dt) o[g][dt] *= alpha;
-    }
-#pragma unroll
-    for (int t = 0; t < C::ST; ++t)
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        u32x4 w;
-        w.x = E::pack2(s[g][t][8 * u + 0], s[g][t][8 * u + 1]);
-        w.y = E::pack2(s[g][t][8 * u + 2], s[g][t][8 * u + 3]);
-        w.z = E::pack2(s[g][t][8 * u + 4], s[g][t][8 * u + 5]);
-        w.w = E::pack2(s[g][t][8 * u + 6], s[g][t][8 * u + 7]);
-        pf[g][2 * t + u] = w;
-      }
+    for (int dt = 0; dt < C::DT; ++dt) o[dt] *= alpha;
+    m = mn;
   }
+}
 
+// p = exp2(s * scale_log2 - m), l += sum(p) in fp32, P packed to the input
+// dtype as the B operands of the PV product (k-step 2 t + u = s[t][8 u .. 8 u + 7]).
+template <class C>
+__device__ __forceinline__ void softmax_pack(const f32x16 (&s)[C::ST], float m, float& l,
+                                             float scale_log2, u32x4 (&pf)[C::KS]) {
+  using E = Elem<C::BF16>;
+  const float neg_m = -m;
+  float e[C::ST][16];
+  float rs = 0.0f;
 #pragma unroll
-  for (int dt = 0; dt < C::DT; ++dt) {
-    const unsigned char* va = vt + ln.v_base + 64 * (dt ^ ln.vy);
+  for (int t = 0; t < C::ST; ++t)
 #pragma unroll
-    for (int k2 = 0; k2 < C::KS; ++k2) {
-      const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          FGW_LDS(i16x4, va + (16 * k2) * C::ROW_BYTES));
-      const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          FGW_LDS(i16x4, va + (16 * k2 + 8) * C::ROW_BYTES));
-      const u32x2 lo2 = __builtin_bit_cast(u32x2, lo), hi2 = __builtin_bit_cast(u32x2, hi);
-      const u32x4 a = {lo2.x, lo2.y, hi2.x, hi2.y};
-#pragma unroll
-      for (int g = 0; g < C::QG; ++g) o[g][dt] = E::mma(a, pf[g][k2], o[g][dt]);
+    for (int v = 0; v < 16; ++v) {
+      e[t][v] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][v], scale_log2, neg_m));
+      rs += e[t][v];
     }
+  l += rs;
+#pragma unroll
+  for (int t = 0; t < C::ST; ++t)
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      u32x4 w;
+      w.x = E::pack2(e[t][8 * u + 0], e[t][8 * u + 1]);
+      w.y = E::pack2(e[t][8 * u + 2], e[t][8 * u + 3]);
+      w.z = E::pack2(e[t][8 * u + 4], e[t][8 * u + 5]);
+      w.w = E::pack2(e[t][8 * u + 6], e[t][8 * u + 7]);
+      pf[2 * t + u] = w;
+    }
+}
+
+// O^T += V^T P^T for one block, V^T operands read one step ahead.
+template <class C>
+__device__ __forceinline__ void pv_block(const unsigned char* vt, const Lanes<C>& ln,
+                                         const u32x4 (&pf)[C::KS], f32x16 (&o)[C::DT]) {
+  using E = Elem<C::BF16>;
+  constexpr int NSTEP = C::DT * C::KS;  // step j: k2 = j / DT, dt = j % DT
+  u32x4 va[2];
+  va[0] = read_vt<C>(vt, ln, 0, 0);
+#pragma unroll
+  for (int j = 0; j < NSTEP; ++j) {
+    if (j + 1 < NSTEP) va[(j + 1) & 1] = read_vt<C>(vt, ln, (j + 1) % C::DT, (j + 1) / C::DT);
+    o[j % C::DT] = E::mma(va[j & 1], pf[j / C::DT], o[j % C::DT]);
   }
 }
 
@@ -410,6 +482,7 @@ __global__ __launch_bounds__(C::THREADS) void fwd_kernel(FwdParams p,
   unsigned char* const group_base = smem + wk * C::GROUP_BYTES;
   const Lanes<C> ln(lane);
   const int64_t row_bytes = (int64_t)p.heads * p.dim * 2;
+  const DmaLanes<C> dl(lane, wq, row_bytes);
 
   const int grid = gridDim.x;
   const int prog = xcd_remap(blockIdx.x, grid);
@@ -442,23 +515,17 @@ __global__ __launch_bounds__(C::THREADS) void fwd_kernel(FwdParams p,
     const int cnt = blk_end - blk_begin;
     const int my_n = cnt > wk ? (cnt - wk + C::NWK - 1) / C::NWK : 0;
 
+    // Rows of this wave and their visible key counts; blocks that end above
+    // wmin hold keys some row of the wave cannot see and are masked.
     const int row_base = q0 + wq * C::ROWS_WAVE;
-    const bool wave_active = row_base < p.sq;
-    const int wave_last = (row_base + C::ROWS_WAVE < p.sq ? row_base + C::ROWS_WAVE : p.sq) - 1;
     int wmin = p.causal ? len - p.sq + row_base + 1 : len;
     wmin = wmin < 0 ? 0 : (wmin > len ? len : wmin);
-    int wmax = p.causal ? len - p.sq + wave_last + 1 : len;
-    wmax = wmax < 0 ? 0 : (wmax > len ? len : wmax);
+    const int qrow = row_base + il;
+    int vis = p.causal ? len - p.sq + qrow + 1 : len;
+    vis = vis < 0 ? 0 : (vis > len ? len : vis);
 
-    u32x4 qf[C::QG][C::KK];
-    int vis[C::QG];
-    float m[C::QG], l[C::QG];
-    f32x16 o[C::QG][C::DT];
-#pragma unroll
-    for (int g = 0; g < C::QG; ++g) {
-      const int qrow = row_base + 32 * g + il;
-      int vv = p.causal ? len - p.sq + qrow + 1 : len;
-      vis[g] = vv < 0 ? 0 : (vv > len ? len : vv);
+    u32x4 qf[C::KK];
+    {
       const u16* qp =
           static_cast<const u16*>(p.q) + (((int64_t)b * p.sq + qrow) * p.heads + h) * p.dim;
 #pragma unroll
@@ -466,25 +533,29 @@ __global__ __launch_bounds__(C::THREADS) void fwd_kernel(FwdParams p,
         const int d = 16 * kk + 8 * hh;
         u32x4 val = {0u, 0u, 0u, 0u};
         if (qrow < p.sq && d < p.dim) val = load16(qp + d);
-        qf[g][kk] = val;
+        qf[kk] = val;
       }
-      m[g] = kNegBig;
-      l[g] = 0.0f;
-#pragma unroll
-      for (int dt = 0; dt < C::DT; ++dt)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) o[g][dt][v] = 0.0f;
     }
+    float m = kNegBig, l = 0.0f;
+    f32x16 o[C::DT];
+#pragma unroll
+    for (int dt = 0; dt < C::DT; ++dt)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) o[dt][v] = 0.0f;
 
-    // Block n of this key group starts at key (blk_begin + wk + NWK n) * BN.
-    // Page ids are read one block ahead of their DMA issue.
     constexpr int kStep = C::NWK * C::BN;
     const int first_pos = (blk_begin + wk) * C::BN;
-    int32_t next_id = my_n > 1 ? page_id(p, table_b, first_pos + kStep) : 0;
     __syncthreads();  // LDS of the previous work item is no longer read
+    // Every key group streams its blocks n = 0, 1, ... at key
+    // (blk_begin + wk + NWK n) * BN through its own LDS stages; the DMA of
+    // block n + 1 is in flight while block n is computed.
+    int32_t next_id = my_n > 1 ? page_id(p, table_b, first_pos + kStep) : 0;
     if (my_n > 0) {
-      issue_block<C>(p, table_b, kb, vb, row_bytes, first_pos, page_id(p, table_b, first_pos),
-                     len, group_base, group_base + C::TILE_BYTES, wq, lane);
+      const int32_t id0 = page_id(p, table_b, first_pos);
+      issue_tile<C, false>(p, dl, table_b, kb, row_bytes, first_pos, id0, len, group_base, wq,
+                           lane);
+      issue_tile<C, true>(p, dl, table_b, vb, row_bytes, first_pos, id0, len,
+                          group_base + C::TILE_BYTES, wq, lane);
     }
     for (int n = 0; n < my_n; ++n) {
       const int pos0 = first_pos + kStep * n;
@@ -495,42 +566,43 @@ __global__ __launch_bounds__(C::THREADS) void fwd_kernel(FwdParams p,
       if (n + 2 < my_n) next_id = page_id(p, table_b, pos0 + 2 * kStep);
       if (n + 1 < my_n && C::NBUF == 2) {
         unsigned char* next = group_base + ((n + 1) % C::NBUF) * C::STAGE_BYTES;
-        issue_block<C>(p, table_b, kb, vb, row_bytes, pos0 + kStep, id1, len, next,
-                       next + C::TILE_BYTES, wq, lane);
+        issue_tile<C, false>(p, dl, table_b, kb, row_bytes, pos0 + kStep, id1, len, next, wq,
+                             lane);
+        issue_tile<C, true>(p, dl, table_b, vb, row_bytes, pos0 + kStep, id1, len,
+                            next + C::TILE_BYTES, wq, lane);
       }
-      if (wave_active && pos0 < wmax) {
-        compute_block<C>(stage, stage + C::TILE_BYTES, ln, qf, o, m, l, vis, pos0,
-                         pos0 + C::BN > wmin, p.scale_log2, hh);
-      }
+      f32x16 s[C::ST];
+      u32x4 pf[C::KS];
+      qk_block<C>(stage, ln, qf, s);
+      if (pos0 + C::BN > wmin) mask_block<C>(s, pos0, vis, hh);
+      update_ref<C>(row_max<C>(s, p.scale_log2), m, l, o);
+      softmax_pack<C>(s, m, l, p.scale_log2, pf);
+      pv_block<C>(stage + C::TILE_BYTES, ln, pf, o);
       if (n + 1 < my_n && C::NBUF == 1) {
         group_sync<C>();  // single stage: refill only after every wave has read it
-        issue_block<C>(p, table_b, kb, vb, row_bytes, pos0 + kStep, id1, len, stage,
-                       stage + C::TILE_BYTES, wq, lane);
+        issue_tile<C, false>(p, dl, table_b, kb, row_bytes, pos0 + kStep, id1, len, stage, wq,
+                             lane);
+        issue_tile<C, true>(p, dl, table_b, vb, row_bytes, pos0 + kStep, id1, len,
+                            stage + C::TILE_BYTES, wq, lane);
       }
     }
 
     if constexpr (C::NWK == 1) {
+      const float tot = l + __shfl_xor(l, 32);
+      if (qrow < p.sq) {
+        const float inv = 1.0f / fmaxf(tot, 1.0e-30f);
 #pragma unroll
-      for (int g = 0; g < C::QG; ++g) {
-        const float tot = l[g] + __shfl_xor(l[g], 32);
-        const int qrow = row_base + 32 * g + il;
-        if (qrow < p.sq) {
-          const float inv = 1.0f / fmaxf(tot, 1.0e-30f);
+        for (int dt = 0; dt < C::DT; ++dt)
 #pragma unroll
-          for (int dt = 0; dt < C::DT; ++dt)
-#pragma unroll
-            for (int gq = 0; gq < 4; ++gq) {
-              const int d0 = 32 * dt + 8 * gq + 4 * hh;
-              if (d0 < p.dim) {
-                f32x4 val = {o[g][dt][4 * gq], o[g][dt][4 * gq + 1], o[g][dt][4 * gq + 2],
-                             o[g][dt][4 * gq + 3]};
-                store_row<C>(p, b, h, split, qrow, d0, val, inv);
-              }
+          for (int gq = 0; gq < 4; ++gq) {
+            const int d0 = 32 * dt + 8 * gq + 4 * hh;
+            if (d0 < p.dim) {
+              f32x4 val = {o[dt][4 * gq], o[dt][4 * gq + 1], o[dt][4 * gq + 2], o[dt][4 * gq + 3]};
+              store_row<C>(p, b, h, split, qrow, d0, val, inv);
             }
-          if (p.mode == 1 && hh == 0) {
-            p.lse[(((int64_t)b * p.heads + h) * p.splits + split) * p.sq + qrow] =
-                lse_of(m[g], tot);
           }
+        if (p.mode == 1 && hh == 0) {
+          p.lse[(((int64_t)b * p.heads + h) * p.splits + split) * p.sq + qrow] = lse_of(m, tot);
         }
       }
     } else {
@@ -539,45 +611,40 @@ __global__ __launch_bounds__(C::THREADS) void fwd_kernel(FwdParams p,
       float* cm = reinterpret_cast<float*>(smem);
       float* cl = cm + C::NWK * C::ROWS_WAVE;
       float* co = cl + C::NWK * C::ROWS_WAVE;
-#pragma unroll
-      for (int g = 0; g < C::QG; ++g) {
-        const float tot = l[g] + __shfl_xor(l[g], 32);
-        const int r = 32 * g + il;
-        if (hh == 0) {
-          cm[wk * C::ROWS_WAVE + r] = m[g];
-          cl[wk * C::ROWS_WAVE + r] = tot;
-        }
-#pragma unroll
-        for (int dt = 0; dt < C::DT; ++dt)
-#pragma unroll
-          for (int gq = 0; gq < 4; ++gq) {
-            f32x4 val = {o[g][dt][4 * gq], o[g][dt][4 * gq + 1], o[g][dt][4 * gq + 2],
-                         o[g][dt][4 * gq + 3]};
-            *reinterpret_cast<f32x4*>(co + (wk * C::ROWS_WAVE + r) * C::OSTRIDE + 32 * dt +
-                                      8 * gq + 4 * hh) = val;
-          }
+      const float tot = l + __shfl_xor(l, 32);
+      if (hh == 0) {
+        cm[wk * C::ROWS_WAVE + il] = m;
+        cl[wk * C::ROWS_WAVE + il] = tot;
       }
+#pragma unroll
+      for (int dt = 0; dt < C::DT; ++dt)
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+          f32x4 val = {o[dt][4 * gq], o[dt][4 * gq + 1], o[dt][4 * gq + 2], o[dt][4 * gq + 3]};
+          *reinterpret_cast<f32x4*>(co + (wk * C::ROWS_WAVE + il) * C::OSTRIDE + 32 * dt +
+                                    8 * gq + 4 * hh) = val;
+        }
       __syncthreads();
       constexpr int D4 = C::DPAD / 4;
       for (int idx = tid; idx < C::ROWS_WAVE * D4; idx += C::THREADS) {
         const int r = idx / D4, d0 = 4 * (idx % D4);
-        const int qrow = q0 + r;
-        if (qrow < p.sq && d0 < p.dim) {
+        const int row = q0 + r;
+        if (row < p.sq && d0 < p.dim) {
           float mm = kNegBig;
 #pragma unroll
           for (int k = 0; k < C::NWK; ++k) mm = fmaxf(mm, cm[k * C::ROWS_WAVE + r]);
-          float tot = 0.0f;
+          float t2 = 0.0f;
           f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
           for (int k = 0; k < C::NWK; ++k) {
             const float wt = __builtin_amdgcn_exp2f(cm[k * C::ROWS_WAVE + r] - mm);
-            tot += cl[k * C::ROWS_WAVE + r] * wt;
+            t2 += cl[k * C::ROWS_WAVE + r] * wt;
             acc += *reinterpret_cast<const f32x4*>(co + (k * C::ROWS_WAVE + r) * C::OSTRIDE + d0) *
                    wt;
           }
-          store_row<C>(p, b, h, split, qrow, d0, acc, 1.0f / fmaxf(tot, 1.0e-30f));
+          store_row<C>(p, b, h, split, row, d0, acc, 1.0f / fmaxf(t2, 1.0e-30f));
           if (p.mode == 1 && d0 == 0) {
-            p.lse[(((int64_t)b * p.heads + h) * p.splits + split) * p.sq + qrow] = lse_of(mm, tot);
+            p.lse[(((int64_t)b * p.heads + h) * p.splits + split) * p.sq + row] = lse_of(mm, t2);
           }
         }
       }
