@@ -7,6 +7,13 @@ kernel included, compile and H2D excluded), as the reference times it
 (benchmarks/mha/bench_mha_mfu.py:221-247). Alongside: Q1 decode at KV32768
 in us/call and HBM GB/s.
 
+Every launch inside the timed region is bracketed by its own pair of events on
+the launching stream, so the roofline's kernel duration is the mean over the
+same K launches that give `value`. `traffic` (HBM bytes per launch) comes from
+the rocprofv3 FETCH_SIZE / WRITE_SIZE summary under profiles/, scaled by the
+same counters read for a plain copy of known size (`--copy-probe` is that
+copy).
+
 Prints one JSON line. `python bench.py --gpus N` with N > 1 exits: the build
 runs on one GPU.
 """
@@ -14,8 +21,8 @@ from __future__ import annotations
 
 import argparse
 import json
-import os
 import pathlib
+import re
 import statistics
 import sys
 import time
@@ -26,6 +33,8 @@ sys.path.insert(0, str(ROOT))
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
 METRIC = "MFU% + TFLOP/s (Q4096) and µs/call + HBM GB/s (Q1 decode), 1 MI355X"
+TRAFFIC_SUMMARY = ROOT / "profiles" / "hbm_traffic_q4096_kv2048_and_q1_kv32768.md"
+COPY_PROBE_BYTES = 1 << 30
 
 
 def parse():
@@ -34,28 +43,36 @@ def parse():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--samples", type=int, default=51, help="single-call event samples per workload")
-    ap.add_argument("--cpu-threads", type=int, default=0, help="0 = all host cores")
+    ap.add_argument("--cpu-threads", type=int, default=0, help="0 = torch's default thread count")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="wall-clock bound of the CPU baseline sample at full thread count")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only run a plain 1 GiB device copy (counter calibration) and exit")
     return ap.parse_args()
 
 
-def timed_steps(call, steps, warmup):
-    """Total ms of exactly `steps` calls, bracketed by device synchronisation."""
+def timed_region(call, steps, warmup):
+    """Run `warmup` untimed calls, then exactly `steps` calls between two device
+    synchronisations. Each call is bracketed by its own events on the current
+    stream. Returns (total ms, per-call ms list)."""
     import torch
     for _ in range(warmup):
         call()
     torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(steps):
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(2 * steps)]
+    for i in range(steps):
+        marks[2 * i].record()
         call()
-    end.record()
+        marks[2 * i + 1].record()
     torch.cuda.synchronize()
-    return start.elapsed_time(end)
+    total = marks[0].elapsed_time(marks[-1])
+    per_call = [marks[2 * i].elapsed_time(marks[2 * i + 1]) for i in range(steps)]
+    return total, per_call
 
 
-def call_samples(call, samples):
-    """Per-call event durations (ms) on the launching stream, reference style."""
+def single_calls(call, samples):
+    """Isolated single-call event durations (ms), the reference's statistic."""
     import torch
     out = []
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -68,32 +85,59 @@ def call_samples(call, samples):
     return out
 
 
-def cpu_reference_timed(inputs, page, threads, reps):
+def cpu_timed(inputs, page, threads, budget_s, min_reps=3):
+    """Median wall-clock seconds of the oracle's chunked CPU attention, repeated
+    until `budget_s` seconds have passed (at least `min_reps` runs)."""
     import torch
     from oracle import mha_oracle as O
     torch.set_num_threads(threads)
-    times, out = [], None
-    for _ in range(reps):
+    times, out, spent = [], None, 0.0
+    while len(times) < min_reps or spent < budget_s:
         t0 = time.perf_counter()
         out = O.chunked_reference(*inputs, page, False, 128)
         times.append(time.perf_counter() - t0)
-    return statistics.median(times), out
+        spent += times[-1]
+    return statistics.median(times), len(times), out
+
+
+def traffic_from_profile(kernel_key):
+    """HBM bytes per launch recorded in the committed rocprofv3 summary (or None)."""
+    if not TRAFFIC_SUMMARY.exists():
+        return None
+    pat = re.compile(rf"^traffic_bytes\[{re.escape(kernel_key)}\]:\s*(\d+)\s*$", re.M)
+    m = pat.search(TRAFFIC_SUMMARY.read_text())
+    return int(m.group(1)) if m else None
+
+
+def copy_probe():
+    import torch
+    n = COPY_PROBE_BYTES // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes": COPY_PROBE_BYTES, "launches": 5}), flush=True)
+    return 0
 
 
 def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU; --gpus {args.gpus} is not supported by this build "
-              "(paged MHA work items are independent; see DESIGN.md for how it would shard)",
-              file=sys.stderr)
+              "(every GPU box here has one GPU; work items are independent and would shard "
+              "by (batch, head) with no exchange)", file=sys.stderr)
         return 2
     import torch
+    torch.cuda.set_device(0)
+    if args.copy_probe:
+        return copy_probe()
     from fgw_amd.operators.mha.current import build_kernel
     from oracle import mha_oracle as O
 
-    torch.cuda.set_device(0)
     dev = torch.device("cuda", 0)
-    cores = args.cpu_threads or os.cpu_count() or 1
+    cores = args.cpu_threads or torch.get_num_threads()
+    rtol, atol = O.TOLERANCES[torch.bfloat16]
 
     # ---- headline: Q4096 / KV2048 prefill ------------------------------
     b, sq, h, d, page, kv = 2, 4096, 8, 128, 128, 2048
@@ -106,28 +150,27 @@ def main():
     torch.cuda.synchronize()
 
     cpu = None
-    expected = None
     if not args.no_cpu_baseline:
-        cpu_s, expected = cpu_reference_timed(host, page, cores, 3)
+        cpu_s, reps, expected = cpu_timed(host, page, cores, args.cpu_seconds)
+        cpu4_s, reps4, _ = cpu_timed(host, page, 4, args.cpu_seconds / 2)
         cpu = {"value": flops / cpu_s / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
-               "sample": f"full Q4096/KV2048 B2H8 D128 workload, oracle chunked_reference "
-                         f"(torch fp32, chunk 128) at torch.set_num_threads({cores}), median of 3",
-               "seconds_per_call": cpu_s}
-        # Four threads: the reference harness's CPU cap (resource_guard.py:14-20).
-        cpu4_s, _ = cpu_reference_timed(host, page, 4, 1)
-        cpu["value_4_threads"] = flops / cpu4_s / 1e12
+               "sample": f"whole Q4096/KV2048 B2H8 D128 workload, oracle chunked_reference "
+                         f"(torch fp32, chunk 128), median of {reps} runs at "
+                         f"torch.set_num_threads({cores}); value_4_threads: median of {reps4} runs "
+                         f"at 4 threads (the reference harness cap)",
+               "seconds_per_call": cpu_s, "value_4_threads": flops / cpu4_s / 1e12}
     else:
         expected = O.chunked_reference(*host, page, False, 128)
-    rtol, atol = O.TOLERANCES[torch.bfloat16]
     torch.testing.assert_close(got.cpu(), expected, rtol=rtol, atol=atol)
 
     call = lambda: kern(*inputs)  # noqa: E731
-    total_ms = timed_steps(call, args.steps, args.warmup)
+    total_ms, per_call = timed_region(call, args.steps, args.warmup)
     ms = total_ms / args.steps
-    samples = call_samples(call, args.samples)
-    kernel_ms = statistics.mean(samples)
+    kernel_ms = statistics.mean(per_call)  # direct mode: one kernel per call
     tflops = flops / (ms * 1e-3) / 1e12
     achieved = flops / (kernel_ms * 1e-3) / 1e12
+    samples = single_calls(call, args.samples)
+    qkv_bytes = O.algorithmic_bytes([kv] * b, sq, h, d, kv // page)
 
     # ---- decode: Q1 / KV32768 -------------------------------------------
     db, dsq, dkv = 2, 1, 32768
@@ -141,26 +184,28 @@ def main():
     torch.testing.assert_close(dgot.cpu(), dexp, rtol=rtol, atol=atol)
     dbytes = O.algorithmic_bytes([dkv] * db, dsq, h, d, dkv // page)
     dcall = lambda: dkern(*dinputs)  # noqa: E731
-    timed_steps(dcall, 20, 20)
-    dsamples = call_samples(dcall, args.samples)
-    d_us = statistics.median(dsamples) * 1e3
+    d_total, _ = timed_region(dcall, args.steps, args.warmup)
+    d_us = statistics.median(single_calls(dcall, args.samples)) * 1e3
     decode = {"workload": "Q1/KV32768 B2H8 D128 BF16 page128", "us_per_call": d_us,
-              "gbs": dbytes / (d_us * 1e-6) / 1e9, "bytes": dbytes,
-              "num_splits": dkern.num_splits, "grid": dkern.compute_grid}
+              "gbs": dbytes / (d_us * 1e-6) / 1e9,
+              "us_per_call_back_to_back": d_total / args.steps * 1e3,
+              "bytes": dbytes, "num_splits": dkern.num_splits, "grid": dkern.compute_grid,
+              "execution_mode": dkern.execution_mode}
     if dkern.execution_mode == "split_and_merge":
         pcall = lambda: dkern.partial_kernel(*dinputs)  # noqa: E731
-        timed_steps(pcall, 20, 20)
-        p_ms = statistics.mean(call_samples(pcall, args.samples))
+        _, p_per_call = timed_region(pcall, args.steps, args.warmup)
+        p_ms = statistics.mean(p_per_call)
         p_achieved = dbytes / (p_ms * 1e-3) / 1e9
-        decode["roofline"] = {"bound": "hbm", "kernel": "fwd_kernel (partial)",
+        p_traffic = traffic_from_profile("decode_partial")
+        decode["roofline"] = {"bound": "hbm", "kernel": "fwd_kernel (partial, key layout)",
                               "achieved": p_achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                              "frac": p_achieved / PEAK_HBM_GBS, "traffic": None}
+                              "frac": p_achieved / PEAK_HBM_GBS, "traffic": p_traffic,
+                              "kernel_us": p_ms * 1e3}
     if not args.no_cpu_baseline:
-        t0 = time.perf_counter()
-        O.chunked_reference(*dhost, page, False, 128)
-        c_s = time.perf_counter() - t0
+        c_s, creps, _ = cpu_timed(dhost, page, cores, args.cpu_seconds / 4, min_reps=3)
         decode["cpu_baseline"] = {"value": dbytes / c_s / 1e9, "unit": "GB/s", "cores": cores,
-                                  "kind": "port", "sample": "full Q1/KV32768 workload, 1 run"}
+                                  "kind": "port",
+                                  "sample": f"whole Q1/KV32768 workload, median of {creps} runs"}
 
     line = {
         "metric": METRIC, "value": tflops, "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
@@ -171,10 +216,12 @@ def main():
                    "page_size": page, "num_splits": kern.num_splits, "grid": kern.compute_grid,
                    "layout": kern.layout},
         "mfu_percent": 100.0 * tflops / PEAK_BF16_TFLOPS,
-        "median_call_us": statistics.median(samples) * 1e3,
-        "roofline": {"bound": "mfma", "kernel": "fwd_kernel (direct)", "achieved": achieved,
-                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS,
-                     "traffic": None},
+        "median_single_call_us": statistics.median(samples) * 1e3,
+        "roofline": {"bound": "mfma", "kernel": "fwd_kernel (direct, query layout)",
+                     "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": achieved / PEAK_BF16_TFLOPS,
+                     "traffic": traffic_from_profile("prefill_direct"),
+                     "algorithmic_bytes": qkv_bytes, "kernel_us": kernel_ms * 1e3},
         "cpu_baseline": cpu,
         "decode": decode,
     }

@@ -231,3 +231,15 @@ def test_gather_packed_matches_explicit_rows():
                 assert torch.equal(ok[b, pos], k[row]) and torch.equal(ov[b, pos], v[row])
             else:
                 assert torch.count_nonzero(ok[b, pos]) == 0
+
+
+def test_bench_inputs_recipe_properties():
+    q, k, v, table, lengths = O.bench_inputs(2, 3, 4, 16, 8, 40, torch.bfloat16)
+    assert q.shape == (2, 3, 4, 16) and k.shape == (2 * 5 * 8, 4, 16) == v.shape
+    assert table.dtype == torch.int32 and lengths.tolist() == [40, 40]
+    # The table is a shuffle of all pool pages: every page is read exactly once.
+    assert sorted(table.flatten().tolist()) == list(range(10))
+    again = O.bench_inputs(2, 3, 4, 16, 8, 40, torch.bfloat16)
+    assert all(torch.equal(a, b) for a, b in zip((q, k, v, table), again[:4]))
+    other = O.bench_inputs(2, 3, 4, 16, 8, 40, torch.bfloat16, seed=8)
+    assert not torch.equal(table, other[3]) or not torch.equal(q, other[0])
