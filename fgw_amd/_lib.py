@@ -10,11 +10,12 @@ import pathlib
 import threading
 
 LIBRARY = pathlib.Path(__file__).resolve().with_name("libfgw_mha.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 FGW_MHA_OK, FGW_MHA_EINVAL, FGW_MHA_EUNSUPPORTED, FGW_MHA_EHIP = 0, -1, -2, -3
 DTYPE_FLOAT16, DTYPE_BFLOAT16 = 0, 1
-LAYOUT_AUTO, LAYOUT_QUERY, LAYOUT_KEY = -1, 0, 1
+LAYOUT_AUTO, LAYOUT_QUERY, LAYOUT_KEY, LAYOUT_PREFILL = -1, 0, 1, 2
+NUM_LAYOUTS = 3
 
 c_int32, c_int64, c_void_p = ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p
 
@@ -30,7 +31,7 @@ class Request(ctypes.Structure):
 
 
 class DeviceInfo(ctypes.Structure):
-    _fields_ = [("num_cus", c_int32), ("wg_per_cu", c_int32 * 2), ("arch_gfx950", c_int32)]
+    _fields_ = [("num_cus", c_int32), ("wg_per_cu", c_int32 * NUM_LAYOUTS), ("arch_gfx950", c_int32)]
 
 
 class Plan(ctypes.Structure):

@@ -10,6 +10,7 @@
 #include "../../include/fgw_mha.h"
 #include "fmha_aux.h"
 #include "fmha_kernel.h"
+#include "fmha_prefill.h"
 #include "fmha_registry.h"
 
 namespace fgw_mha {
@@ -18,16 +19,26 @@ FGW_MHA_FOR_DPAD_LO(FGW_MHA_EXTERN, true)
 FGW_MHA_FOR_DPAD_HI(FGW_MHA_EXTERN, true)
 FGW_MHA_FOR_DPAD_LO(FGW_MHA_EXTERN, false)
 FGW_MHA_FOR_DPAD_HI(FGW_MHA_EXTERN, false)
+FGW_MHA_FOR_PREFILL_LO(FGW_MHA_EXTERN_PREFILL, true)
+FGW_MHA_FOR_PREFILL_HI(FGW_MHA_EXTERN_PREFILL, true)
+FGW_MHA_FOR_PREFILL_LO(FGW_MHA_EXTERN_PREFILL, false)
+FGW_MHA_FOR_PREFILL_HI(FGW_MHA_EXTERN_PREFILL, false)
 
 #define FGW_ENTRY(BF, DP, LY) \
   if (bf16 == BF && dpad == DP && layout == LY) return FwdEntry{&launch_fwd<BF, DP, LY>, &occupancy_fwd<BF, DP, LY>};
 #define FGW_ENTRIES(BF, DP) FGW_ENTRY(BF, DP, kLayoutQuery) FGW_ENTRY(BF, DP, kLayoutKey)
+#define FGW_PREFILL_ENTRY(BF, DP) \
+  if (bf16 == BF && dpad == DP && layout == kLayoutPrefill) return FwdEntry{&launch_prefill<BF, DP>, &occupancy_prefill<BF, DP>};
 
 FwdEntry fwd_entry(bool bf16, int dpad, int layout) {
   FGW_MHA_FOR_DPAD_LO(FGW_ENTRIES, true)
   FGW_MHA_FOR_DPAD_HI(FGW_ENTRIES, true)
   FGW_MHA_FOR_DPAD_LO(FGW_ENTRIES, false)
   FGW_MHA_FOR_DPAD_HI(FGW_ENTRIES, false)
+  FGW_MHA_FOR_PREFILL_LO(FGW_PREFILL_ENTRY, true)
+  FGW_MHA_FOR_PREFILL_HI(FGW_PREFILL_ENTRY, true)
+  FGW_MHA_FOR_PREFILL_LO(FGW_PREFILL_ENTRY, false)
+  FGW_MHA_FOR_PREFILL_HI(FGW_PREFILL_ENTRY, false)
   return FwdEntry{nullptr, nullptr};
 }
 
@@ -72,9 +83,18 @@ constexpr int kMaxSplits = 128;
 constexpr int kAutoMaxSplits = 64;
 constexpr int kMinRoundsPerSplit = 2;
 
-// Keys one program consumes per loop round, per layout.
-int keys_per_round(int layout) { return layout == kLayoutQuery ? 64 : 4 * 32; }
-int rows_per_tile(int layout) { return layout == kLayoutQuery ? 128 : 32; }
+// Keys one program consumes per loop round, and query rows per work item,
+// per layout.
+int keys_per_round(int layout) { return layout == kLayoutKey ? 4 * 32 : 64; }
+int rows_per_tile(int layout) {
+  return layout == kLayoutKey ? 32 : (layout == kLayoutPrefill ? 256 : 128);
+}
+// Head-dim tiles with a prefill-layout kernel.
+bool has_prefill(int dpad) { return dpad == 64 || dpad == 128; }
+// The automatic layout choice uses the prefill layout only when asked for
+// explicitly; it is not yet faster than the query layout on MI355X.
+constexpr bool kAutoPrefill = false;
+constexpr int kPrefillMinSq = 129;
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
@@ -112,8 +132,10 @@ int check_shape(const fgw_mha_shape* s) {
 
 int check_plan(const fgw_mha_shape* s, const fgw_mha_plan_t* p) {
   if (!p) return fail(FGW_MHA_EINVAL, "plan is NULL");
-  if (p->layout != kLayoutQuery && p->layout != kLayoutKey)
+  if (p->layout != kLayoutQuery && p->layout != kLayoutKey && p->layout != kLayoutPrefill)
     return fail(FGW_MHA_EINVAL, "plan layout %d is not a kernel layout", p->layout);
+  if (p->layout == kLayoutPrefill && !has_prefill(dim_tile(s->dim)))
+    return fail(FGW_MHA_EINVAL, "the prefill layout needs D in (32, 128]");
   const int rows = rows_per_tile(p->layout);
   const int q_tiles = (s->sq + rows - 1) / rows;
   const int64_t tasks = (int64_t)s->batch * s->heads * q_tiles;
@@ -212,7 +234,7 @@ int fgw_mha_query_device(int device, fgw_mha_device_info* info) {
     return hip_fail(err, "hipSetDevice");
   info->num_cus = prop.multiProcessorCount;
   info->arch_gfx950 = std::strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : 0;
-  for (int layout = 0; layout < 2; ++layout) {
+  for (int layout = 0; layout < FGW_MHA_NUM_LAYOUTS; ++layout) {
     const int n = fwd_entry(true, 128, layout).occupancy();
     info->wg_per_cu[layout] = n > 0 ? n : 1;
   }
@@ -226,10 +248,18 @@ int fgw_mha_plan(const fgw_mha_shape* s, const fgw_mha_request* req,
   if (rc) return rc;
   if (!req || !dev || !out) return fail(FGW_MHA_EINVAL, "request/device/plan is NULL");
   if (dev->num_cus <= 0) return fail(FGW_MHA_EINVAL, "device info has no compute units");
+  const int dpad = dim_tile(s->dim);
   int layout = req->layout;
-  if (layout == FGW_MHA_LAYOUT_AUTO) layout = s->sq <= 32 ? kLayoutKey : kLayoutQuery;
-  if (layout != kLayoutQuery && layout != kLayoutKey)
-    return fail(FGW_MHA_EINVAL, "layout must be -1 (auto), 0 (query) or 1 (key)");
+  if (layout == FGW_MHA_LAYOUT_AUTO) {
+    layout = s->sq <= 32 ? kLayoutKey
+                         : (kAutoPrefill && s->sq >= kPrefillMinSq && has_prefill(dpad)
+                                ? kLayoutPrefill
+                                : kLayoutQuery);
+  }
+  if (layout != kLayoutQuery && layout != kLayoutKey && layout != kLayoutPrefill)
+    return fail(FGW_MHA_EINVAL, "layout must be -1 (auto), 0 (query), 1 (key) or 2 (prefill)");
+  if (layout == kLayoutPrefill && !has_prefill(dpad))
+    return fail(FGW_MHA_EINVAL, "the prefill layout needs D in (32, 128]");
   const int rows = rows_per_tile(layout);
   const int q_tiles = (s->sq + rows - 1) / rows;
   const int64_t tasks = (int64_t)s->batch * s->heads * q_tiles;
@@ -276,9 +306,9 @@ int fgw_mha_plan(const fgw_mha_shape* s, const fgw_mha_request* req,
   out->query_tile_tasks = (int32_t)tasks;
   out->work_items = (int32_t)work;
   out->grid = (int32_t)grid;
-  out->threads = 256;
+  out->threads = layout == kLayoutPrefill ? 512 : 256;
   out->execution_mode = splits > 1 ? 1 : 0;
-  out->dim_padded = dim_tile(s->dim);
+  out->dim_padded = dpad;
   out->parts_floats = splits > 1 ? (int64_t)s->batch * s->heads * splits * s->sq * s->dim : 0;
   out->lse_floats = splits > 1 ? (int64_t)s->batch * s->heads * splits * s->sq : 0;
   return FGW_MHA_OK;

@@ -1,7 +1,9 @@
 // Forward-kernel instantiations: f16, head-dim tiles of the lo half.
 #include "fmha_kernel.h"
+#include "fmha_prefill.h"
 #include "fmha_registry.h"
 
 namespace fgw_mha {
 FGW_MHA_FOR_DPAD_LO(FGW_MHA_INSTANTIATE, false)
+FGW_MHA_FOR_PREFILL_LO(FGW_MHA_INSTANTIATE_PREFILL, false)
 }  // namespace fgw_mha

@@ -185,6 +185,54 @@ struct Cfg {
   static_assert(LDS_BYTES <= kLdsBudget, "LDS budget of one CU");
 };
 
+// LDS DMA (global_load_lds_dwordx4) for kernels that place their own waits
+// (fmha_prefill.h) is issued by inline assembly: the compiler then neither
+// counts these loads nor treats them as LDS writes (it would otherwise wait
+// for every outstanding DMA before each transposing LDS read), and the
+// kernels wait for them explicitly with wait_vm. The compiler's own vmcnt
+// waits stay correct: loads retire in order, so extra loads it does not know
+// of can only make its waits stricter. fwd_kernel uses the compiler builtin.
+// Byte address of a shared-memory pointer within the workgroup's LDS.
+__device__ __forceinline__ u32 lds_address(const void* p) {
+  return (u32)(uintptr_t)FGW_LDS(const void, p);
+}
+
+// One DMA instruction: 64 lanes x 16 bytes into LDS [lds, lds + 1024).
+// `base` and `lds` are uniform across the wave; readfirstlane places them in
+// SGPRs where the compiler cannot prove that by itself. The hazards the
+// compiler cannot see inside the assembly are covered by nops: one wait
+// state between the M0 write and the LDS DMA, and five between a VALU write
+// of the base SGPRs (readfirstlane) and the load that reads them.
+// The assembly clobbers M0, which the compiler uses for nothing else in these
+// kernels (it does not preserve M0 across inline assembly).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ u32 uniform_u32(u32 x) { return __builtin_amdgcn_readfirstlane(x); }
+// Uniform global base + per-lane 32-bit offset (saddr form).
+__device__ __forceinline__ void dma_saddr(const void* base, u32 voff, u32 lds) {
+  const uint64_t b = (uint64_t)base;
+  const uint64_t ub = ((uint64_t)uniform_u32((u32)(b >> 32)) << 32) | uniform_u32((u32)b);
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 4\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(voff), "s"(ub), "s"(uniform_u32(lds))
+               : "memory", "m0");
+}
+// Per-lane 64-bit global address.
+__device__ __forceinline__ void dma_flat(const void* addr, u32 lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(addr), "s"(uniform_u32(lds))
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// Wait until at most N vector-memory loads of this wave are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+
 // Synchronise the waves that share one key group's tiles.
 template <class C>
 __device__ __forceinline__ void group_sync() {
@@ -198,7 +246,7 @@ __device__ __forceinline__ void group_sync() {
 }
 
 // Wait for this wave's outstanding DMA loads (vmcnt = 0; lgkm and exp untouched).
-__device__ __forceinline__ void wait_dma() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+__device__ __forceinline__ void wait_dma() { wait_vm<0>(); }
 
 // Per-lane DMA offsets. Instruction i of a stage fills slots 64 i + lane:
 // key row RPI i + lr (lr = lane / CPR), position pos = lane % CPR, which
@@ -587,6 +635,7 @@ __global__ __launch_bounds__(C::THREADS) void fwd_kernel(FwdParams p,
       }
     }
 
+    wait_dma();  // no DMA of this work item outlives it
     if constexpr (C::NWK == 1) {
       const float tot = l + __shfl_xor(l, 32);
       if (qrow < p.sq) {

@@ -9,6 +9,7 @@ namespace fgw_mha {
 enum Layout : int {
   kLayoutQuery = 0,  // 4 waves split the query rows of a tile and share K/V tiles
   kLayoutKey = 1,    // 4 waves split the key blocks of a work item (decode)
+  kLayoutPrefill = 2,  // 8 waves x 32 query rows, pipelined K/V rings (fmha_prefill.h)
 };
 
 struct FwdParams {

@@ -36,6 +36,15 @@ hipError_t launch_gather(const GatherParams& p, hipStream_t stream);
   template hipError_t launch_fwd<BF, DP, kLayoutKey>(const FwdParams&, int, hipStream_t);   \
   template int occupancy_fwd<BF, DP, kLayoutQuery>();                                       \
   template int occupancy_fwd<BF, DP, kLayoutKey>();
+// The prefill layout exists for head-dim tiles 64 and 128.
+#define FGW_MHA_FOR_PREFILL_LO(X, BF) X(BF, 64)
+#define FGW_MHA_FOR_PREFILL_HI(X, BF) X(BF, 128)
+#define FGW_MHA_INSTANTIATE_PREFILL(BF, DP)                                   \
+  template hipError_t launch_prefill<BF, DP>(const FwdParams&, int, hipStream_t); \
+  template int occupancy_prefill<BF, DP>();
+#define FGW_MHA_EXTERN_PREFILL(BF, DP)                                               \
+  extern template hipError_t launch_prefill<BF, DP>(const FwdParams&, int, hipStream_t); \
+  extern template int occupancy_prefill<BF, DP>();
 #define FGW_MHA_EXTERN(BF, DP)                                                                     \
   extern template hipError_t launch_fwd<BF, DP, kLayoutQuery>(const FwdParams&, int, hipStream_t); \
   extern template hipError_t launch_fwd<BF, DP, kLayoutKey>(const FwdParams&, int, hipStream_t);   \

@@ -32,7 +32,9 @@ ROUTE = "hip_mfma"
 PERSISTENT_DEVICE = "device"  # cap the grid at the device's resident workgroups
 SPLIT_POLICIES = ("auto", "legacy", "cost_model")
 _DTYPES = {"float16": torch.float16, "bfloat16": torch.bfloat16}
-_LAYOUTS = {None: _lib.LAYOUT_AUTO, "query": _lib.LAYOUT_QUERY, "key": _lib.LAYOUT_KEY}
+_LAYOUTS = {None: _lib.LAYOUT_AUTO, "query": _lib.LAYOUT_QUERY, "key": _lib.LAYOUT_KEY,
+            "prefill": _lib.LAYOUT_PREFILL}
+_LAYOUT_NAMES = {_lib.LAYOUT_QUERY: "query", _lib.LAYOUT_KEY: "key", _lib.LAYOUT_PREFILL: "prefill"}
 
 
 def _dtype_name(dtype) -> str:
@@ -93,7 +95,7 @@ class _Launch:
         self.query_tile_tasks = plan.query_tile_tasks
         self.execution_mode = "split_and_merge" if plan.execution_mode else "direct_single_split"
         self.execution_path = ROUTE
-        self.layout = "key" if plan.layout == _lib.LAYOUT_KEY else "query"
+        self.layout = _LAYOUT_NAMES[plan.layout]
         self.dim_padded = plan.dim_padded
         # Q is read in place as [B, Sq, H, D]; no head-major copy is needed.
         self.prepare_q = lambda q: q
@@ -182,8 +184,9 @@ def build_kernel(batch, sq, heads, dim, pool_rows, width, page_size, causal, dty
     persistent_programs (v7_experimental.py:29-30: None = uncapped grid; here
     the default caps the grid at the device's resident workgroups),
     cache_lengths (host-known lengths for the cost model,
-    cube_general.py:17, :45) and layout ("query" = waves split query rows,
-    "key" = waves split key blocks; None chooses by Sq).
+    cube_general.py:17, :45) and layout ("query" = 4 waves split 128 query
+    rows, "prefill" = 8 waves split 256 query rows with pipelined K/V rings,
+    D in (32, 128]; "key" = waves split key blocks; None chooses by Sq).
     """
     requested_split_policy = split_policy
     if split_policy not in SPLIT_POLICIES:
@@ -204,7 +207,7 @@ def build_kernel(batch, sq, heads, dim, pool_rows, width, page_size, causal, dty
                        _lib.DTYPE_BFLOAT16 if name == "bfloat16" else _lib.DTYPE_FLOAT16)
     persistent = _persistent_request(persistent_programs)
     if layout not in _LAYOUTS:
-        raise ValueError("layout must be None, 'query' or 'key'")
+        raise ValueError("layout must be None, 'query', 'key' or 'prefill'")
 
     if num_splits is not None:
         splits, policy = num_splits, "explicit"

@@ -35,13 +35,14 @@ FEATURE_NAMES = ("constant", "wave_rounds", "waves", "has_merge", "partial_mbyte
                  "longest_excess")
 
 
-def geometry(sq: int):
-    """(layout index, rows per tile, keys per round) of the planner's layout choice."""
+def geometry(sq: int, dim: int = 128):
+    """(layout index, rows per tile, keys per round) of the planner's automatic
+    layout choice (fgw_mha_plan: key layout for Sq <= 32, else query layout)."""
     return (1, 32, 128) if sq <= 32 else (0, 128, 64)
 
 
 def features(batch, sq, heads, dim, lengths: Sequence[int], splits, num_cus, wg_per_cu):
-    layout, rows, keys_round = geometry(sq)
+    layout, rows, keys_round = geometry(sq, dim)
     tasks = batch * heads * math.ceil(sq / rows)
     slots = max(1, num_cus * max(1, wg_per_cu[layout]))
     waves = math.ceil(tasks * splits / slots)

@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define FGW_MHA_ABI_VERSION 1
+#define FGW_MHA_ABI_VERSION 2
 
 typedef enum {
   FGW_MHA_OK = 0,
@@ -52,8 +52,11 @@ typedef enum { FGW_MHA_FLOAT16 = 0, FGW_MHA_BFLOAT16 = 1 } fgw_mha_dtype;
 typedef enum {
   FGW_MHA_LAYOUT_AUTO = -1,
   FGW_MHA_LAYOUT_QUERY = 0, /* 4 waves x 32 query rows share 64-key K/V tiles (prefill) */
-  FGW_MHA_LAYOUT_KEY = 1    /* 4 waves split the keys of 32 query rows (decode) */
+  FGW_MHA_LAYOUT_KEY = 1,   /* 4 waves split the keys of 32 query rows (decode) */
+  FGW_MHA_LAYOUT_PREFILL = 2 /* 8 waves x 32 query rows, pipelined K/V rings; D in (32, 128] */
 } fgw_mha_layout;
+
+#define FGW_MHA_NUM_LAYOUTS 3
 
 /* Static shape of one operator instance: the arguments of the reference
  * build_kernel (v7.py:32-47) that fix a specialisation. */
@@ -80,7 +83,7 @@ typedef struct {
 /* Device facts the planner needs; filled by fgw_mha_query_device. */
 typedef struct {
   int32_t num_cus;          /* compute units */
-  int32_t wg_per_cu[2];     /* resident workgroups per CU, per layout, for dim = 128 */
+  int32_t wg_per_cu[FGW_MHA_NUM_LAYOUTS]; /* resident workgroups per CU, per layout, dim 128 */
   int32_t arch_gfx950;      /* 1 when the device is gfx950 */
 } fgw_mha_device_info;
 

@@ -11,7 +11,7 @@ from fgw_amd import _lib
 
 ROOT = pathlib.Path(__file__).resolve().parents[1]
 HEADER = ROOT / "include" / "fgw_mha.h"
-DEVICE = _lib.DeviceInfo(256, (ctypes.c_int32 * 2)(2, 2), 1)
+DEVICE = _lib.DeviceInfo(256, (ctypes.c_int32 * _lib.NUM_LAYOUTS)(2, 2, 1), 1)
 
 
 @pytest.fixture(scope="module")
@@ -45,6 +45,13 @@ def test_plan_headline_shapes(lib):
     prefill = _lib.plan(shape(sq=4096, kv=2048), _lib.Request(0, -1, -1), DEVICE)
     assert (prefill.layout, prefill.rows_per_tile, prefill.q_tiles, prefill.num_splits) == (0, 128, 32, 1)
     assert (prefill.work_items, prefill.grid, prefill.execution_mode) == (512, 512, 0)
+    assert prefill.threads == 256
+    mid = _lib.plan(shape(sq=128, kv=2048), _lib.Request(0, -1, -1), DEVICE)
+    assert (mid.layout, mid.rows_per_tile) == (0, 128)  # up to 128 queries: query layout
+    wide = _lib.plan(shape(sq=4096, kv=2048, d=256), _lib.Request(0, -1, -1), DEVICE)
+    assert (wide.layout, wide.dim_padded) == (0, 256)  # no prefill kernel for D > 128
+    narrow = _lib.plan(shape(sq=4096, kv=2048, d=32), _lib.Request(0, -1, -1), DEVICE)
+    assert narrow.layout == 0
     decode = _lib.plan(shape(sq=1, kv=32768), _lib.Request(0, -1, -1), DEVICE)
     assert (decode.layout, decode.rows_per_tile, decode.num_splits, decode.work_items) == (1, 32, 32, 512)
     assert decode.parts_floats == 2 * 8 * 32 * 1 * 128 and decode.lse_floats == 2 * 8 * 32
@@ -66,6 +73,10 @@ def test_plan_split_rules(lib):
     assert explicit.num_splits == 16 and explicit.execution_mode == 1
     forced = _lib.plan(shape(sq=64, kv=8192), _lib.Request(0, -1, _lib.LAYOUT_KEY), DEVICE)
     assert (forced.layout, forced.q_tiles) == (1, 2)
+    pre = _lib.plan(shape(sq=64, kv=8192), _lib.Request(0, -1, _lib.LAYOUT_PREFILL), DEVICE)
+    assert (pre.layout, pre.q_tiles, pre.rows_per_tile) == (2, 1, 256)
+    with pytest.raises(ValueError, match="prefill layout"):
+        _lib.plan(shape(sq=512, d=256), _lib.Request(0, -1, _lib.LAYOUT_PREFILL), DEVICE)
     for bad in (3, 256, -2):
         with pytest.raises(ValueError, match="num_splits"):
             _lib.plan(shape(), _lib.Request(bad, -1, -1), DEVICE)

@@ -134,7 +134,7 @@ def test_layouts_and_persistent_grids_agree():
         dev = [x.cuda() for x in (q, k, v, table, lengths)]
         expected = O.reference(q, k, v, table, lengths, 64, causal)
         outs = []
-        for layout in ("query", "key"):
+        for layout in ("query", "key", "prefill"):
             for persistent in (None, 1, 7, "device"):
                 kern = build_kernel(2, 40, 4, 128, k.shape[0], 20, 64, causal, "bfloat16", 0,
                                     num_splits=2, persistent_programs=persistent, layout=layout)
