@@ -43,12 +43,14 @@ FwdEntry fwd_entry(bool bf16, int dpad, int layout) {
 }
 
 hipError_t launch_merge(bool bf16, const MergeParams& p, hipStream_t stream) {
-  const int64_t rows = (int64_t)p.batch * p.sq * p.heads;
-  const dim3 grid((unsigned)((rows + 3) / 4));
+  // One (row, 4 dims) pair per thread: a workgroup covers whole rows.
+  const int rows_per_wg = (4 * kMergeThreads) / p.dim > 0 ? (4 * kMergeThreads) / p.dim : 1;
+  const int64_t groups = (p.sq + rows_per_wg - 1) / rows_per_wg;
+  const dim3 grid((unsigned)((int64_t)p.batch * p.heads * groups));
   if (bf16) {
-    merge_kernel<true><<<grid, dim3(256), 0, stream>>>(p);
+    merge_kernel<true><<<grid, dim3(kMergeThreads), 0, stream>>>(p, rows_per_wg);
   } else {
-    merge_kernel<false><<<grid, dim3(256), 0, stream>>>(p);
+    merge_kernel<false><<<grid, dim3(kMergeThreads), 0, stream>>>(p, rows_per_wg);
   }
   return hipGetLastError();
 }

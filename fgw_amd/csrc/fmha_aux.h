@@ -4,50 +4,77 @@
 
 namespace fgw_mha {
 
-// Combine the split partials of one output row (b, q, h) per wave:
+// LSE merge of the split partials of output rows [q0, q0 + rows) of (b, h),
+// one (row, 4 dims) pair per thread:
 //   peak = max over splits with LSE > -1e29,
 //   w_s  = LSE_s > -1e29 ? exp(LSE_s - peak) : 0,
 //   O    = sum_s w_s * Part_s / max(sum_s w_s, 1e-30), cast to the input dtype.
-// This is the reference merge (v7.py:352-370, cube_general.py:259-278) with
-// the running peak taken in a first pass over the LSE values; empty splits
-// (LSE -1e30) carry zero weight and an all-empty row is exactly zero.
+// This is the reference merge (v7.py:352-370, cube_general.py:259-278):
+// splits are taken in chunks of kMergeChunk whose loads are all issued before
+// any is used (one memory round trip per chunk), and the running peak moves
+// once per chunk. Empty splits (LSE -1e30) carry zero weight and an
+// all-empty row is exactly zero.
+constexpr int kMergeChunk = 16;
 template <bool BF16>
-__global__ __launch_bounds__(256) void merge_kernel(MergeParams p) {
+__device__ __forceinline__ void merge_rows(const float* parts, const float* lse, void* out, int sq,
+                                           int heads, int dim, int splits, int b, int h, int q0,
+                                           int rows, int tid, int nthreads) {
   using E = Elem<BF16>;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  const int64_t rows = (int64_t)p.batch * p.sq * p.heads;
-  if (row >= rows) return;
-  const int h = (int)(row % p.heads);
-  const int64_t bq = row / p.heads;
-  const int q = (int)(bq % p.sq);
-  const int b = (int)(bq / p.sq);
-  const int64_t bhs = ((int64_t)b * p.heads + h) * p.splits;
-
-  float peak = kNegBig;
-  for (int s = 0; s < p.splits; ++s) {
-    const float x = p.lse[(bhs + s) * p.sq + q];
-    if (x > -1.0e29f) peak = fmaxf(peak, x);
-  }
-  const int d0 = lane * 4;
-  float tot = 0.0f;
-  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int s = 0; s < p.splits; ++s) {
-    const float x = p.lse[(bhs + s) * p.sq + q];
-    const float wgt = x > -1.0e29f ? expf(x - peak) : 0.0f;
-    tot += wgt;
-    if (wgt != 0.0f && d0 < p.dim) {
-      acc += *reinterpret_cast<const f32x4*>(p.parts + ((bhs + s) * p.sq + q) * p.dim + d0) * wgt;
+  const int d4n = dim / 4;
+  const int64_t bhs = ((int64_t)b * heads + h) * splits;
+  for (int idx = tid; idx < rows * d4n; idx += nthreads) {
+    const int q = q0 + idx / d4n, d0 = 4 * (idx % d4n);
+    const float* ls = lse + bhs * sq + q;
+    const float* ps = parts + (bhs * sq + q) * dim + d0;
+    float peak = kNegBig, tot = 0.0f;
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s0 = 0; s0 < splits; s0 += kMergeChunk) {
+      float x[kMergeChunk];
+      f32x4 v[kMergeChunk];
+#pragma unroll
+      for (int i = 0; i < kMergeChunk; ++i) {
+        const int s = s0 + i < splits ? s0 + i : splits - 1;  // clamped; weight 0 below
+        x[i] = ls[(int64_t)s * sq];
+        v[i] = *reinterpret_cast<const f32x4*>(ps + (int64_t)s * sq * dim);
+      }
+      float cpeak = peak;
+#pragma unroll
+      for (int i = 0; i < kMergeChunk; ++i) {
+        const bool live = s0 + i < splits && x[i] > -1.0e29f;
+        cpeak = live ? fmaxf(cpeak, x[i]) : cpeak;
+      }
+      const float keep = expf(peak - cpeak);  // 0 while nothing was live, 1 if unchanged
+      tot *= keep;
+      acc *= keep;
+#pragma unroll
+      for (int i = 0; i < kMergeChunk; ++i) {
+        const bool live = s0 + i < splits && x[i] > -1.0e29f;
+        const float wgt = live ? expf(x[i] - cpeak) : 0.0f;
+        tot += wgt;
+        acc += live ? v[i] * wgt : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+      peak = cpeak;
     }
-  }
-  if (d0 < p.dim) {
     const float inv = 1.0f / fmaxf(tot, 1.0e-30f);
     u32x2 w;
     w.x = E::pack2(acc[0] * inv, acc[1] * inv);
     w.y = E::pack2(acc[2] * inv, acc[3] * inv);
-    u16* dst = static_cast<u16*>(p.out) + (((int64_t)b * p.sq + q) * p.heads + h) * p.dim + d0;
+    u16* dst = static_cast<u16*>(out) + (((int64_t)b * sq + q) * heads + h) * dim + d0;
     *reinterpret_cast<u32x2*>(dst) = w;
   }
+}
+
+// Stand-alone LSE merge: one workgroup per (b, h, group of rows_per_wg rows).
+constexpr int kMergeThreads = 256;
+template <bool BF16>
+__global__ __launch_bounds__(kMergeThreads) void merge_kernel(MergeParams p, int rows_per_wg) {
+  const int groups = (p.sq + rows_per_wg - 1) / rows_per_wg;
+  const int g = blockIdx.x % groups;
+  const int bh = blockIdx.x / groups;
+  const int q0 = g * rows_per_wg;
+  const int rows = p.sq - q0 < rows_per_wg ? p.sq - q0 : rows_per_wg;
+  merge_rows<BF16>(p.parts, p.lse, p.out, p.sq, p.heads, p.dim, p.splits, bh / p.heads,
+                   bh % p.heads, q0, rows, threadIdx.x, kMergeThreads);
 }
 
 // Packed copy of the live cache: out[b, pos] = cache[phys_row(b, pos)] for

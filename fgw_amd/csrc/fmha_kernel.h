@@ -650,7 +650,7 @@ __global__ __launch_bounds__(C::THREADS) void fwd_kernel(FwdParams p,
               store_row<C>(p, b, h, split, qrow, d0, val, inv);
             }
           }
-        if (p.mode == 1 && hh == 0) {
+        if (p.mode != 0 && hh == 0) {
           p.lse[(((int64_t)b * p.heads + h) * p.splits + split) * p.sq + qrow] = lse_of(m, tot);
         }
       }
@@ -692,7 +692,7 @@ __global__ __launch_bounds__(C::THREADS) void fwd_kernel(FwdParams p,
                    wt;
           }
           store_row<C>(p, b, h, split, row, d0, acc, 1.0f / fmaxf(t2, 1.0e-30f));
-          if (p.mode == 1 && d0 == 0) {
+          if (p.mode != 0 && d0 == 0) {
             p.lse[(((int64_t)b * p.heads + h) * p.splits + split) * p.sq + row] = lse_of(mm, t2);
           }
         }

@@ -61,6 +61,11 @@ def _device_info(index: int) -> _lib.DeviceInfo:
     return _lib.query_device(index)
 
 
+def _current_stream(device: torch.device) -> int:
+    """Raw handle of the current HIP stream of `device`."""
+    return torch.cuda.current_stream(device).cuda_stream
+
+
 def _persistent_request(persistent_programs) -> int:
     if persistent_programs == PERSISTENT_DEVICE:
         return -1
@@ -84,6 +89,10 @@ class _Launch:
         self._kv_shape = (shape.pool_rows, shape.heads, shape.dim)
         self._meta_shapes = ((shape.batch, shape.width), (shape.batch,))
         self._lib = _lib.load()
+        self._fwd = self._lib.fgw_mha_fwd
+        self._shape_ref = ctypes.byref(shape)
+        self._plan_ref = ctypes.byref(plan)
+        self._ws_floats = plan.parts_floats + plan.lse_floats
         self.block_q = plan.rows_per_tile
         self.compute_grid = plan.grid
         self.task_assignment = "contiguous"
@@ -126,23 +135,26 @@ class _Launch:
                             None if lse is None else lse.data_ptr())
 
     def _stream(self):
-        return ctypes.c_void_p(torch.cuda.current_stream(self._device).cuda_stream)
+        return ctypes.c_void_p(_current_stream(self._device))
 
     def _workspace(self):
-        parts = torch.empty(self._plan.parts_floats, dtype=torch.float32, device=self._device)
-        lse = torch.empty(self._plan.lse_floats, dtype=torch.float32, device=self._device)
-        return parts, lse
+        """Partials then LSE, carved from one allocation."""
+        ws = torch.empty(self._ws_floats, dtype=torch.float32, device=self._device)
+        return ws[:self._plan.parts_floats], ws[self._plan.parts_floats:]
 
     # -- public calls --------------------------------------------------------
     def __call__(self, q, k, v, table, lengths):
         self._check(q, k, v, table, lengths)
         out = torch.empty(self._out_shape, dtype=self._dtype, device=self._device)
-        parts = lse = None
+        t = _lib.Tensors(q.data_ptr(), k.data_ptr(), v.data_ptr(), table.data_ptr(),
+                         lengths.data_ptr(), out.data_ptr())
         if self._plan.execution_mode:
-            parts, lse = self._workspace()
-        t = self._tensors(q, k, v, table, lengths, out, parts, lse)
-        _lib.check(self._lib.fgw_mha_fwd(ctypes.byref(self._shape), ctypes.byref(self._plan),
-                                         ctypes.byref(t), self._stream()))
+            ws = torch.empty(self._ws_floats, dtype=torch.float32, device=self._device)
+            t.parts = ws.data_ptr()
+            t.lse = t.parts + 4 * self._plan.parts_floats
+        rc = self._fwd(self._shape_ref, self._plan_ref, ctypes.byref(t), self._stream())
+        if rc:
+            _lib.check(rc)
         return out
 
     def _direct(self, q, k, v, table, lengths):

@@ -209,3 +209,4 @@ def test_headline_shapes():
         expected = O.chunked_reference(q, k, v, table, lengths, p, False, 128)
         r = check_output(got, expected, q, lengths, False, f"B{b} Q{sq} H{h} KV{kv}")
         log(f"B{b} Q{sq} H{h} KV{kv}: splits={kern.num_splits} grid={kern.compute_grid} ratio={r:.3f}")
+
