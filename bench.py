@@ -49,6 +49,15 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 1 GiB device copy (counter calibration) and exit")
+    ap.add_argument("--suite", default="headline",
+                    choices=("headline", "decode-scan", "grid", "prefill", "scans"),
+                    help="headline: the one-line bench contract (default). decode-scan: "
+                         "BASELINE config 4 split scan; grid: config 2 short-Q grid; "
+                         "prefill: Q4096 and Q32768; scans: the three scan suites")
+    ap.add_argument("--out", default=None, help="scan suites: JSONL file for the records "
+                    "(a markdown summary is written beside it)")
+    ap.add_argument("--scan-samples", type=int, default=21)
+    ap.add_argument("--scan-warmup", type=int, default=5)
     return ap.parse_args()
 
 
@@ -121,6 +130,226 @@ def copy_probe():
     return 0
 
 
+# ---------------------------------------------------------------------------
+# Scan suites: one record per configuration, each
+# checked against the oracle before it is timed, as the reference benches do
+# (benchmarks/mha/bench_mha_mfu.py:207-220; bench_v7_split_scan.py:88-120;
+# bench_split_breakdown.py:79-96 for the partial / merge components).
+# ---------------------------------------------------------------------------
+def _time_call(call, samples, warmup):
+    """(median single-call us, mean back-to-back us) of `call`."""
+    back_ms, _ = timed_region(call, samples, warmup)
+    single = statistics.median(single_calls(call, samples)) * 1e3
+    return single, back_ms / samples * 1e3
+
+
+def _components(kern, dinputs, samples, warmup):
+    """Mean per-launch us of the partial kernel and of the merge on fixed partials."""
+    import torch
+    _, p_ms = timed_region(lambda: kern.partial_kernel(*dinputs), samples, warmup)
+    parts, lse = kern.partial_kernel(*dinputs)
+    torch.cuda.synchronize()
+    _, m_ms = timed_region(lambda: kern.merge_kernel(parts, lse), samples, warmup)
+    return statistics.mean(p_ms) * 1e3, statistics.mean(m_ms) * 1e3
+
+
+def _checked(kern, dinputs, expected, dtype, label):
+    import torch
+    from oracle import mha_oracle as O
+    got = kern(*dinputs)
+    torch.cuda.synchronize()
+    rtol, atol = O.TOLERANCES[dtype]
+    torch.testing.assert_close(got.cpu(), expected, rtol=rtol, atol=atol,
+                               msg=lambda m: f"{label}: {m}")
+
+
+def suite_decode_scan(args, emit):
+    """Config 4: B2 H8 D128 page 128, Q in {1, 16} x KV in {512 .. 32768}, FP16 and
+    BF16, splits 1..32 and auto; plus the imbalanced B4 variant."""
+    import torch
+    from fgw_amd.operators.mha.current import build_kernel
+    from oracle import mha_oracle as O
+    dev = torch.device("cuda", 0)
+    b, h, d, page = 2, 8, 128, 128
+    for dtype, name in ((torch.bfloat16, "bf16"), (torch.float16, "fp16")):
+        for sq in (1, 16):
+            for kv in (512, 2048, 8192, 32768):
+                host = O.bench_inputs(b, sq, h, d, page, kv, dtype)
+                dinputs = [x.to(dev) for x in host]
+                expected = O.chunked_reference(*host, page, False, 128)
+                nbytes = O.algorithmic_bytes([kv] * b, sq, h, d, kv // page)
+                for req in (None, 1, 2, 4, 8, 16, 32):
+                    if req is not None and req > kv // 32:
+                        continue
+                    kern = build_kernel(b, sq, h, d, host[1].shape[0], kv // page, page, False,
+                                        name.replace("bf16", "bfloat16").replace("fp16", "float16"),
+                                        0, num_splits=req, full_kv_cache=True)
+                    label = f"decode {name} q{sq} kv{kv} splits={req}"
+                    _checked(kern, dinputs, expected, dtype, label)
+                    call = lambda: kern(*dinputs)  # noqa: E731
+                    single, back = _time_call(call, args.scan_samples, args.scan_warmup)
+                    rec = {"suite": "decode-scan", "dtype": name, "batch": b, "heads": h,
+                           "head_dim": d, "q_len": sq, "kv_len": kv, "requested_splits": req,
+                           "num_splits": kern.num_splits, "grid": kern.compute_grid,
+                           "split_policy": kern.split_policy, "us_per_call": single,
+                           "us_back_to_back": back, "hbm_gbs": nbytes / (single * 1e-6) / 1e9}
+                    if kern.execution_mode == "split_and_merge":
+                        rec["partial_us"], rec["merge_us"] = _components(
+                            kern, dinputs, args.scan_samples, args.scan_warmup)
+                    emit(rec)
+        # Imbalanced variant: B4, lengths uniform in [KV/8, KV] (seeded), width KV/page.
+        for sq in (1, 16):
+            kv = 8192
+            lengths = torch.randint(kv // 8, kv + 1, (4,), generator=torch.Generator().manual_seed(7))
+            q, k, v, table, _ = O.bench_inputs(4, sq, h, d, page, kv, dtype)
+            host = (q, k, v, table, lengths.to(torch.int32))
+            dinputs = [x.to(dev) for x in host]
+            expected = O.chunked_reference(*host, page, False, 128)
+            nbytes = O.algorithmic_bytes(lengths.tolist(), sq, h, d, kv // page)
+            for req in (None, 1, 4, 16):
+                kern = build_kernel(4, sq, h, d, k.shape[0], kv // page, page, False,
+                                    "bfloat16" if name == "bf16" else "float16", 0,
+                                    num_splits=req)
+                _checked(kern, dinputs, expected, dtype, f"imbalanced {name} q{sq} splits={req}")
+                single, back = _time_call(lambda: kern(*dinputs), args.scan_samples,
+                                          args.scan_warmup)
+                emit({"suite": "decode-imbalanced", "dtype": name, "batch": 4, "heads": h,
+                      "head_dim": d, "q_len": sq, "kv_len": kv, "lengths": lengths.tolist(),
+                      "requested_splits": req, "num_splits": kern.num_splits,
+                      "grid": kern.compute_grid, "us_per_call": single, "us_back_to_back": back,
+                      "hbm_gbs": nbytes / (single * 1e-6) / 1e9})
+
+
+def suite_grid(args, emit):
+    """Config 2: B1 H1 D128 BF16 page 128, Q in {1 .. 512} x KV in {128 .. 16384};
+    each spec as one direct kernel (split 1) and with the automatic split."""
+    import torch
+    from fgw_amd.operators.mha.current import build_kernel
+    from oracle import mha_oracle as O
+    dev = torch.device("cuda", 0)
+    for sq in (1, 2, 4, 8, 16, 32, 64, 128, 256, 512):
+        for kv in (128, 256, 512, 1024, 2048, 4096, 8192, 16384):
+            host = O.bench_inputs(1, sq, 1, 128, 128, kv, torch.bfloat16)
+            dinputs = [x.to(dev) for x in host]
+            expected = O.chunked_reference(*host, 128, False, 128)
+            flops = O.useful_flops([kv], sq, 1, 128, False)
+            for req in (1, None):
+                kern = build_kernel(1, sq, 1, 128, host[1].shape[0], kv // 128, 128, False,
+                                    "bfloat16", 0, num_splits=req, full_kv_cache=True)
+                _checked(kern, dinputs, expected, torch.bfloat16, f"grid q{sq} kv{kv} {req}")
+                single, back = _time_call(lambda: kern(*dinputs), args.scan_samples,
+                                          args.scan_warmup)
+                emit({"suite": "grid", "dtype": "bf16", "q_len": sq, "kv_len": kv,
+                      "requested_splits": req, "num_splits": kern.num_splits,
+                      "layout": kern.layout, "grid": kern.compute_grid, "us_per_call": single,
+                      "us_back_to_back": back, "tflops": flops / (single * 1e-6) / 1e12})
+
+
+def suite_prefill(args, emit):
+    """Config 3: B2 H8 D128 BF16 page 128, KV 2048, Q 4096 (headline) and Q 32768."""
+    import torch
+    from fgw_amd.operators.mha.current import build_kernel
+    from oracle import mha_oracle as O
+    dev = torch.device("cuda", 0)
+    for sq in (4096, 32768):
+        host = O.bench_inputs(2, sq, 8, 128, 128, 2048, torch.bfloat16)
+        dinputs = [x.to(dev) for x in host]
+        for layout in (None, "prefill"):
+            kern = build_kernel(2, sq, 8, 128, host[1].shape[0], 16, 128, False, "bfloat16", 0,
+                                full_kv_cache=True, layout=layout)
+            if layout is None:
+                expected = O.chunked_reference(*host, 128, False, 128)
+            _checked(kern, dinputs, expected, torch.bfloat16, f"prefill q{sq} {layout}")
+            flops = O.useful_flops([2048] * 2, sq, 8, 128, False)
+            single, back = _time_call(lambda: kern(*dinputs), args.scan_samples, args.scan_warmup)
+            emit({"suite": "prefill", "dtype": "bf16", "q_len": sq, "kv_len": 2048,
+                  "layout": kern.layout, "grid": kern.compute_grid, "us_per_call": single,
+                  "us_back_to_back": back, "tflops_single": flops / (single * 1e-6) / 1e12,
+                  "tflops_back_to_back": flops / (back * 1e-6) / 1e12,
+                  "mfu_percent": 100.0 * flops / (back * 1e-6) / 1e12 / PEAK_BF16_TFLOPS})
+
+
+def run_scans(args):
+    import torch
+    torch.cuda.set_device(0)
+    suites = {"decode-scan": [suite_decode_scan], "grid": [suite_grid],
+              "prefill": [suite_prefill],
+              "scans": [suite_prefill, suite_decode_scan, suite_grid]}[args.suite]
+    out = open(args.out, "w") if args.out else None
+    records = []
+
+    def emit(rec):
+        records.append(rec)
+        line = json.dumps(rec)
+        print(line, flush=True)
+        if out:
+            out.write(line + "\n")
+            out.flush()
+
+    from fgw_amd.operators.mha.kernels.mha_paged_decode_hip import _device_info
+    info = _device_info(0)
+    emit({"suite": "device", "name": torch.cuda.get_device_properties(0).gcnArchName,
+          "num_cus": info.num_cus, "wg_per_cu": list(info.wg_per_cu)})
+    for fn in suites:
+        fn(args, emit)
+    if out:
+        out.close()
+        pathlib.Path(args.out).with_suffix(".md").write_text(scan_markdown(records))
+    return 0
+
+
+def scan_markdown(records):
+    """Summary tables of the scan records (the figures quoted in the docs)."""
+    lines = []
+    pre = [r for r in records if r["suite"] == "prefill"]
+    if pre:
+        lines += ["## Prefill (B2 H8 D128 BF16 page 128, KV 2048)", "",
+                  "| Q | layout | grid | us/call (single) | us (back-to-back) | TFLOP/s | MFU % |",
+                  "|---|---|---|---|---|---|---|"]
+        lines += [f"| {r['q_len']} | {r['layout']} | {r['grid']} | {r['us_per_call']:.1f} | "
+                  f"{r['us_back_to_back']:.1f} | {r['tflops_back_to_back']:.0f} | "
+                  f"{r['mfu_percent']:.1f} |" for r in pre]
+        lines.append("")
+    dec = [r for r in records if r["suite"] == "decode-scan"]
+    if dec:
+        lines += ["## Decode split scan (B2 H8 D128 page 128)", "",
+                  "| dtype | Q | KV | splits | us/call (single) | us (back-to-back) | partial us "
+                  "| merge us | GB/s (single) |", "|---|---|---|---|---|---|---|---|---|"]
+        for r in dec:
+            sp = f"auto->{r['num_splits']}" if r["requested_splits"] is None else str(r["num_splits"])
+            lines.append(f"| {r['dtype']} | {r['q_len']} | {r['kv_len']} | {sp} | "
+                         f"{r['us_per_call']:.1f} | {r['us_back_to_back']:.1f} | "
+                         f"{r.get('partial_us', float('nan')):.1f} | "
+                         f"{r.get('merge_us', float('nan')):.1f} | {r['hbm_gbs']:.0f} |")
+        lines.append("")
+    imb = [r for r in records if r["suite"] == "decode-imbalanced"]
+    if imb:
+        lines += ["## Imbalanced decode (B4 H8 D128, lengths uniform in [KV/8, KV], KV 8192)", "",
+                  "| dtype | Q | lengths | splits | us/call | GB/s |", "|---|---|---|---|---|---|"]
+        for r in imb:
+            sp = f"auto->{r['num_splits']}" if r["requested_splits"] is None else str(r["num_splits"])
+            lines.append(f"| {r['dtype']} | {r['q_len']} | {r['lengths']} | {sp} | "
+                         f"{r['us_per_call']:.1f} | {r['hbm_gbs']:.0f} |")
+        lines.append("")
+    grid = [r for r in records if r["suite"] == "grid"]
+    if grid:
+        kvs = sorted({r["kv_len"] for r in grid})
+        for req, title in ((1, "split 1 (direct)"), (None, "automatic split")):
+            lines += [f"## Short-Q grid, B1 H1 D128 BF16, us/call, {title}", "",
+                      "| Q \\ KV | " + " | ".join(map(str, kvs)) + " |",
+                      "|---" * (len(kvs) + 1) + "|"]
+            for sq in sorted({r["q_len"] for r in grid}):
+                row = {r["kv_len"]: r for r in grid if r["q_len"] == sq and r["requested_splits"] == req}
+                cells = []
+                for kv in kvs:
+                    r = row.get(kv)
+                    cells.append("" if r is None else (f"{r['us_per_call']:.1f}" + (
+                        f" (s{r['num_splits']})" if req is None else "")))
+                lines.append(f"| {sq} | " + " | ".join(cells) + " |")
+            lines.append("")
+    return "\n".join(lines) + "\n"
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -132,6 +361,8 @@ def main():
     torch.cuda.set_device(0)
     if args.copy_probe:
         return copy_probe()
+    if args.suite != "headline":
+        return run_scans(args)
     from fgw_amd.operators.mha.current import build_kernel
     from oracle import mha_oracle as O
 

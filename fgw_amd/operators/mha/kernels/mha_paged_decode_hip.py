@@ -61,9 +61,14 @@ def _device_info(index: int) -> _lib.DeviceInfo:
     return _lib.query_device(index)
 
 
-def _current_stream(device: torch.device) -> int:
-    """Raw handle of the current HIP stream of `device`."""
-    return torch.cuda.current_stream(device).cuda_stream
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def _current_stream(index: int) -> int:
+    """Raw handle of the current HIP stream of device `index`."""
+    if _raw_stream is not None:
+        return _raw_stream(index)
+    return torch.cuda.current_stream(index).cuda_stream
 
 
 def _persistent_request(persistent_programs) -> int:
@@ -88,6 +93,9 @@ class _Launch:
         self._out_shape = (shape.batch, shape.sq, shape.heads, shape.dim)
         self._kv_shape = (shape.pool_rows, shape.heads, shape.dim)
         self._meta_shapes = ((shape.batch, shape.width), (shape.batch,))
+        self._index = device_index
+        self._sizes = (torch.Size(self._out_shape), torch.Size(self._kv_shape),
+                       torch.Size(self._meta_shapes[0]), torch.Size(self._meta_shapes[1]))
         self._lib = _lib.load()
         self._fwd = self._lib.fgw_mha_fwd
         self._shape_ref = ctypes.byref(shape)
@@ -116,6 +124,22 @@ class _Launch:
 
     # -- helpers -----------------------------------------------------------
     def _check(self, q, k, v, table, lengths):
+        """Shape, dtype, device and layout checks of one call; the fast test
+        passes every valid call, _check_detail names the first violation."""
+        qs, kvs, ts, ls = self._sizes
+        dt, idx, i32 = self._dtype, self._index, torch.int32
+        if (q.shape == qs and k.shape == kvs and v.shape == kvs and table.shape == ts
+                and lengths.shape == ls and q.dtype == dt and k.dtype == dt and v.dtype == dt
+                and table.dtype == i32 and lengths.dtype == i32 and q.get_device() == idx
+                and k.get_device() == idx and v.get_device() == idx
+                and table.get_device() == idx and lengths.get_device() == idx
+                and q.is_contiguous() and k.is_contiguous() and v.is_contiguous()
+                and table.is_contiguous() and lengths.is_contiguous()):
+            return
+        self._check_detail(q, k, v, table, lengths)
+        raise ValueError("contiguous inputs on the same GPU required")
+
+    def _check_detail(self, q, k, v, table, lengths):
         if (tuple(q.shape) != self._out_shape or tuple(k.shape) != self._kv_shape
                 or tuple(v.shape) != self._kv_shape or tuple(table.shape) != self._meta_shapes[0]
                 or tuple(lengths.shape) != self._meta_shapes[1]):
@@ -135,7 +159,7 @@ class _Launch:
                             None if lse is None else lse.data_ptr())
 
     def _stream(self):
-        return ctypes.c_void_p(_current_stream(self._device))
+        return _current_stream(self._index)
 
     def _workspace(self):
         """Partials then LSE, carved from one allocation."""
@@ -146,12 +170,15 @@ class _Launch:
     def __call__(self, q, k, v, table, lengths):
         self._check(q, k, v, table, lengths)
         out = torch.empty(self._out_shape, dtype=self._dtype, device=self._device)
-        t = _lib.Tensors(q.data_ptr(), k.data_ptr(), v.data_ptr(), table.data_ptr(),
-                         lengths.data_ptr(), out.data_ptr())
         if self._plan.execution_mode:
             ws = torch.empty(self._ws_floats, dtype=torch.float32, device=self._device)
-            t.parts = ws.data_ptr()
-            t.lse = t.parts + 4 * self._plan.parts_floats
+            parts = ws.data_ptr()
+            t = _lib.Tensors(q.data_ptr(), k.data_ptr(), v.data_ptr(), table.data_ptr(),
+                             lengths.data_ptr(), out.data_ptr(), parts,
+                             parts + 4 * self._plan.parts_floats)
+        else:
+            t = _lib.Tensors(q.data_ptr(), k.data_ptr(), v.data_ptr(), table.data_ptr(),
+                             lengths.data_ptr(), out.data_ptr())
         rc = self._fwd(self._shape_ref, self._plan_ref, ctypes.byref(t), self._stream())
         if rc:
             _lib.check(rc)
