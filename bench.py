@@ -420,8 +420,8 @@ def main():
     decode = {"workload": "Q1/KV32768 B2H8 D128 BF16 page128", "us_per_call": d_us,
               "gbs": dbytes / (d_us * 1e-6) / 1e9,
               "us_per_call_back_to_back": d_total / args.steps * 1e3,
-              "bytes": dbytes, "num_splits": dkern.num_splits, "grid": dkern.compute_grid,
-              "execution_mode": dkern.execution_mode}
+              "bytes": dbytes, "num_splits": dkern.num_splits, "split_policy": dkern.split_policy,
+              "grid": dkern.compute_grid, "execution_mode": dkern.execution_mode}
     if dkern.execution_mode == "split_and_merge":
         pcall = lambda: dkern.partial_kernel(*dinputs)  # noqa: E731
         _, p_per_call = timed_region(pcall, args.steps, args.warmup)

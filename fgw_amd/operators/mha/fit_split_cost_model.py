@@ -1,0 +1,164 @@
+"""Fit the MI355X split-count model from bench.py scan records (offline, CPU only).
+
+Counterpart of the reference's fitting tools (tools/mha/fit_split_cost_model.py,
+tools/mha/fit_general_split_model.py): the calibration data are the JSONL
+records of `bench.py --suite decode-scan|grid --out FILE` (one record per
+(shape, split) with its measured single-call latency); the model is the
+linear score of split_cost_model.features.
+
+Objective (the reference's, restated): within each case (one shape scanned at
+several split counts) the score differences between candidates should match
+the latency differences, weighted by 1 / best latency of the case, with
+nonnegative weights. Case-constant costs cancel, so the constant feature gets
+weight 0 and scores rank candidates rather than predict absolute latency.
+Solved here with scipy's nonnegative least squares on the stacked differences.
+
+    python -m fgw_amd.operators.mha.fit_split_cost_model SCAN.jsonl [SCAN2.jsonl ...]
+
+writes split_cost_model.json beside split_cost_model.py and prints the
+in-sample evaluation (selected split's latency / best measured latency).
+"""
+from __future__ import annotations
+
+import argparse
+import collections
+import hashlib
+import json
+import math
+import pathlib
+from typing import Dict, List
+
+import numpy as np
+from scipy.optimize import nnls
+
+from fgw_amd.operators.mha import split_cost_model as M
+
+SUITES = ("decode-scan", "decode-imbalanced", "grid")
+
+
+class _Device:
+    def __init__(self, num_cus, wg_per_cu):
+        self.num_cus = num_cus
+        self.wg_per_cu = tuple(wg_per_cu)
+
+
+def load_cases(paths) -> tuple:
+    """Cases {key: {"shape": ..., "lat": {splits: us}}} and the scan device."""
+    cases: Dict[tuple, dict] = collections.OrderedDict()
+    device = None
+    for path in paths:
+        for line in pathlib.Path(path).read_text().splitlines():
+            rec = json.loads(line)
+            if rec["suite"] == "device":
+                dev = (rec["num_cus"], tuple(rec["wg_per_cu"]))
+                if device is not None and device != dev:
+                    raise ValueError("scan files come from different devices")
+                device = dev
+                continue
+            if rec["suite"] not in SUITES:
+                continue
+            batch = rec.get("batch", 1)
+            heads = rec.get("heads", 1)
+            dim = rec.get("head_dim", 128)
+            lengths = tuple(rec.get("lengths") or [rec["kv_len"]] * batch)
+            key = (rec["suite"], rec["dtype"], batch, heads, dim, rec["q_len"], rec["kv_len"],
+                   lengths)
+            case = cases.setdefault(key, {"batch": batch, "heads": heads, "dim": dim,
+                                          "sq": rec["q_len"], "capacity": rec["kv_len"],
+                                          "lengths": lengths, "lat": {}, "legacy": None})
+            s = rec["num_splits"]
+            case["lat"][s] = min(case["lat"].get(s, math.inf), rec["us_per_call"])
+            if rec.get("requested_splits") is None:
+                case["legacy"] = s  # the automatic choice when the scan was taken
+    if device is None:
+        raise ValueError("scan records carry no device record")
+    return [c for c in cases.values() if len(c["lat"]) >= 2], _Device(*device)
+
+
+def fit(cases, device) -> List[float]:
+    rows, target = [], []
+    for c in cases:
+        best = min(c["lat"].values())
+        base_s = min(c["lat"])  # smallest measured split as the reference candidate
+        f0 = np.array(M.features(c["batch"], c["sq"], c["heads"], c["dim"], c["lengths"], base_s,
+                                 device.num_cus, device.wg_per_cu))
+        for s, t in c["lat"].items():
+            if s == base_s:
+                continue
+            f = np.array(M.features(c["batch"], c["sq"], c["heads"], c["dim"], c["lengths"], s,
+                                    device.num_cus, device.wg_per_cu))
+            rows.append((f - f0) / best)
+            target.append((t - c["lat"][base_s]) / best)
+    a, y = np.array(rows), np.array(target)
+    scale = np.linalg.norm(a, axis=0)
+    scale[scale == 0] = 1.0
+    w, _ = nnls(a / scale, y)
+    return (w / scale).tolist()
+
+
+def evaluate(weights, cases, device, tolerance, margin) -> dict:
+    model = {"weights": weights, "selection_tolerance": tolerance, "absolute_margin_us": margin}
+    ratios, legacy, rows = [], [], []
+    for c in cases:
+        preds = {s: M.predict(c["batch"], c["sq"], c["heads"], c["dim"], c["lengths"], s,
+                              device.num_cus, device.wg_per_cu, model) for s in c["lat"]}
+        lo = min(preds.values())
+        limit = lo + max(abs(lo) * tolerance, margin)
+        chosen = min(s for s, v in preds.items() if v <= limit)
+        best_s = min(c["lat"], key=c["lat"].get)
+        r = c["lat"][chosen] / c["lat"][best_s]
+        ratios.append(r)
+        if c["legacy"] is not None:
+            legacy.append(c["lat"][c["legacy"]] / c["lat"][best_s])
+        rows.append({"batch": c["batch"], "heads": c["heads"], "sq": c["sq"],
+                     "kv": c["capacity"], "chosen": chosen, "best": best_s,
+                     "relative_to_best": round(r, 4)})
+    geo = lambda xs: math.exp(sum(map(math.log, xs)) / len(xs))  # noqa: E731
+    return {"cases": len(ratios), "within_5pct": sum(r <= 1.05 for r in ratios),
+            "geomean_relative_to_best": geo(ratios), "max_relative_to_best": max(ratios),
+            "legacy_cases": len(legacy),
+            "legacy_geomean_relative_to_best": geo(legacy) if legacy else None,
+            "legacy_max_relative_to_best": max(legacy) if legacy else None, "rows": rows}
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__,
+                                 formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("scans", nargs="+", help="bench.py scan JSONL files")
+    ap.add_argument("--output", default=str(M.MODEL_PATH))
+    ap.add_argument("--tolerance", type=float, default=0.03,
+                    help="relative score tolerance: the smallest split within it wins")
+    ap.add_argument("--margin-us", type=float, default=0.5)
+    args = ap.parse_args(argv)
+    cases, device = load_cases(args.scans)
+    weights = fit(cases, device)
+    report = evaluate(weights, cases, device, args.tolerance, args.margin_us)
+    lens = [c["capacity"] for c in cases]
+    sqs = [c["sq"] for c in cases]
+    model = {
+        "version": 1,
+        "device": {"num_cus": device.num_cus, "wg_per_cu": list(device.wg_per_cu)},
+        "feature_names": list(M.FEATURE_NAMES),
+        "weights": weights,
+        "selection_tolerance": args.tolerance,
+        "absolute_margin_us": args.margin_us,
+        "scope": {"num_cus": device.num_cus, "min_kv": min(lens), "max_kv": max(lens),
+                  "min_sq": min(sqs), "max_sq": max(sqs),
+                  "dims": sorted({c["dim"] for c in cases})},
+        "training_cases": report["cases"],
+        "in_sample": {k: v for k, v in report.items() if k != "rows"},
+        "sources": [{"name": pathlib.Path(p).name,
+                     "sha256": hashlib.sha256(pathlib.Path(p).read_bytes()).hexdigest()}
+                    for p in args.scans],
+        "fit": "nonnegative least squares on within-case latency differences against the "
+               "smallest scanned split, weighted by 1 / best latency of the case",
+    }
+    pathlib.Path(args.output).write_text(json.dumps(model, indent=2) + "\n")
+    print(json.dumps({k: v for k, v in model.items() if k not in ("sources",)}, indent=2))
+    worst = sorted(report["rows"], key=lambda r: -r["relative_to_best"])[:8]
+    print("worst cases:", json.dumps(worst))
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

@@ -254,7 +254,8 @@ def build_kernel(batch, sq, heads, dim, pool_rows, width, page_size, causal, dty
         if split_policy == "auto":
             use_model = split_cost_model.eligible_config(
                 batch, sq, heads, dim, width * page_size, page_size=page_size, causal=causal,
-                full_kv_cache=full_kv_cache, num_cus=device.num_cus)
+                full_kv_cache=full_kv_cache, num_cus=device.num_cus,
+                lengths_known=cache_lengths is not None)
             split_policy = "cost_model" if use_model else "legacy"
         if split_policy == "cost_model":
             lengths = cache_lengths
@@ -307,5 +308,5 @@ def mha_paged_decode(q, k_cache, v_cache, block_table, cache_seqlens, page_size,
                               bool(is_causal), "float16" if q.dtype == torch.float16 else "bfloat16",
                               q.device.index, num_splits=num_splits, split_policy=split_policy,
                               full_kv_cache=full_kv_cache, persistent_programs=persistent_programs,
-                              cache_lengths=tuple(lengths) if split_policy == "cost_model" else None)
+                              cache_lengths=None if full_kv_cache else tuple(lengths))
         return kernel(*inputs)

@@ -70,13 +70,15 @@ def load_model(path: str = str(MODEL_PATH)) -> Optional[dict]:
 
 
 def eligible_config(batch, sq, heads, dim, kv_tokens, *, page_size, causal, full_kv_cache,
-                    num_cus) -> bool:
-    """Automatic policy guard: the calibrated scope of the frozen model."""
+                    num_cus, lengths_known=False) -> bool:
+    """Automatic policy guard: the calibrated scope of the frozen model (non-causal,
+    the calibrated device, table capacity, query length and head dim); the cache
+    lengths must be known on the host (a full cache, or ragged lengths passed in)."""
     model = load_model()
     if model is None:
         return False
     scope = model["scope"]
-    return (not causal and num_cus == scope["num_cus"] and full_kv_cache
+    return (not causal and num_cus == scope["num_cus"] and (full_kv_cache or lengths_known)
             and scope["min_kv"] <= kv_tokens <= scope["max_kv"]
             and scope["min_sq"] <= sq <= scope["max_sq"] and dim in scope["dims"])
 

@@ -1,0 +1,95 @@
+"""MI355X split cost model (fgw_amd/operators/mha/split_cost_model.py), CPU only.
+
+The committed model is pinned to the committed calibration scans: refitting
+them reproduces its weights, and on every scanned case its choice is within a
+few percent of the best measured split (the reference's evaluation metric,
+tools/mha/fit_split_cost_model.py `relative_to_best`). Known answers are the
+best measured split of representative scanned shapes.
+"""
+import json
+import pathlib
+
+import pytest
+
+from fgw_amd.operators.mha import fit_split_cost_model as F
+from fgw_amd.operators.mha import split_cost_model as M
+
+CALIBRATION = pathlib.Path(M.__file__).with_name("calibration") / "mi355x_split_scan.jsonl"
+
+
+class Dev:
+    num_cus = 256
+    wg_per_cu = (2, 1, 1)
+
+
+@pytest.fixture(scope="module")
+def model():
+    m = M.load_model()
+    assert m is not None, "the MI355X calibration is committed"
+    return m
+
+
+def test_committed_model_is_well_formed(model):
+    assert model["feature_names"] == list(M.FEATURE_NAMES)
+    assert all(w >= 0 for w in model["weights"])
+    assert model["scope"]["num_cus"] == 256 and model["scope"]["dims"] == [128]
+    assert model["device"]["wg_per_cu"] == list(Dev.wg_per_cu)
+
+
+def test_refit_reproduces_committed_weights(model):
+    cases, device = F.load_cases([CALIBRATION])
+    weights = F.fit(cases, device)
+    for got, want in zip(weights, model["weights"]):
+        assert got == pytest.approx(want, rel=1e-6, abs=1e-9)
+
+
+def test_choice_is_near_best_on_every_calibrated_case(model):
+    cases, device = F.load_cases([CALIBRATION])
+    report = F.evaluate(model["weights"], cases, device, model["selection_tolerance"],
+                        model["absolute_margin_us"])
+    assert report["cases"] >= 80
+    assert report["max_relative_to_best"] <= 1.05
+    assert report["geomean_relative_to_best"] <= report["legacy_geomean_relative_to_best"]
+
+
+@pytest.mark.parametrize("batch,sq,heads,kv,best", [
+    (2, 1, 8, 32768, 16),    # Q1 decode headline: 16 splits fill 256 CUs
+    (2, 1, 8, 512, 1),       # short cache: the merge launch costs more than it saves
+    (2, 16, 8, 8192, 16),
+    (1, 1, 1, 16384, 64),    # B1H1: one task needs many splits
+])
+def test_known_answers_from_the_scans(model, batch, sq, heads, kv, best):
+    assert M.select_splits(batch, sq, heads, 128, kv, (kv,) * batch, Dev(), model) == best
+
+
+def test_ragged_lengths_shift_the_choice(model):
+    full = M.select_splits(4, 1, 8, 128, 8192, (8192,) * 4, Dev(), model)
+    ragged = M.select_splits(4, 1, 8, 128, 8192, (4635, 4285, 4326, 1917), Dev(), model)
+    assert ragged <= full
+
+
+def test_eligibility_scope(model):
+    kw = dict(page_size=128, num_cus=256)
+    assert M.eligible_config(2, 1, 8, 128, 32768, causal=False, full_kv_cache=True, **kw)
+    assert not M.eligible_config(2, 1, 8, 128, 32768, causal=True, full_kv_cache=True, **kw)
+    assert not M.eligible_config(2, 1, 8, 64, 32768, causal=False, full_kv_cache=True, **kw)
+    assert not M.eligible_config(2, 4096, 8, 128, 2048, causal=False, full_kv_cache=True, **kw)
+    assert not M.eligible_config(2, 1, 8, 128, 65536, causal=False, full_kv_cache=True, **kw)
+    assert not M.eligible_config(2, 1, 8, 128, 8192, causal=False, full_kv_cache=False, **kw)
+    assert M.eligible_config(2, 1, 8, 128, 8192, causal=False, full_kv_cache=False,
+                             lengths_known=True, **kw)
+    assert not M.eligible_config(2, 1, 8, 128, 8192, causal=False, full_kv_cache=True,
+                                 page_size=128, num_cus=304)
+
+
+def test_select_rejects_bad_lengths(model):
+    with pytest.raises(ValueError, match="cache_lengths"):
+        M.select_splits(2, 1, 8, 128, 512, (512,), Dev(), model)
+    with pytest.raises(ValueError, match="cache_lengths"):
+        M.select_splits(1, 1, 8, 128, 512, (513,), Dev(), model)
+
+
+def test_calibration_file_is_scan_records():
+    recs = [json.loads(x) for x in CALIBRATION.read_text().splitlines()]
+    assert recs[0]["suite"] == "device" and recs[0]["num_cus"] == 256
+    assert {r["suite"] for r in recs[1:]} >= {"decode-scan", "grid", "decode-imbalanced"}
