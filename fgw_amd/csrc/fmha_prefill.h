@@ -73,21 +73,39 @@ struct PCfg {
 // Instruction q of the wave fills LDS [dst + 1024 i, + 1024) with
 // i = q * NWQ + wave. Fast case: the block lies in one page, below len,
 // inside the pool, with D == DPAD; its instructions read a uniform tile base
-// plus the wave's fixed per-lane offsets, and the caller issues them later
-// (tile_base returns the base). Otherwise every key row is resolved through
-// the table, masked chunks (key >= len, d >= D, page id outside the pool)
-// read the zero chunk, and the instructions are issued here.
-template <class C, bool IS_V>
-__device__ __forceinline__ const char* tile_base(const FwdParams& p, const char* base,
-                                                 int64_t row_bytes, int pos0, int32_t id0,
-                                                 int len) {
+// plus the wave's fixed per-lane offsets (DmaBatch::issue). Otherwise every
+// key row is resolved through the table and masked chunks (key >= len,
+// d >= D, page id outside the pool) read the zero chunk (issue_slow_tile).
+// Pool byte offset (row * row_bytes) of the first key row of block j of a
+// work item (keys key0 + j BN ..), or -1 when the block needs the per-key
+// path (it straddles a page or len, leaves the pool, or D < DPAD). Blocks
+// j >= N are never loaded and read -1. Evaluated per lane, one block per lane.
+template <class C>
+__device__ __forceinline__ int64_t block_offset(const FwdParams& p, const int32_t* table_b,
+                                                int64_t row_bytes, int key0, int N, int len,
+                                                int j) {
   const u32 page = (u32)p.page_size;
-  const u32 pg0 = div_page((u32)pos0, p.page_magic, p.page_shift);
+  const int pos0 = key0 + j * C::BN;
+  const bool live = j < N;
+  const u32 pg0 = live ? div_page((u32)pos0, p.page_magic, p.page_shift) : 0u;
   const u32 off0 = (u32)pos0 - pg0 * page;
-  const int64_t row0 = (int64_t)id0 * page + off0;
-  const bool fast = off0 + C::BN <= page && pos0 + C::BN <= len && row0 >= 0 &&
+  const int64_t row0 = (int64_t)table_b[pg0] * page + off0;
+  const bool fast = live && off0 + C::BN <= page && pos0 + C::BN <= len && row0 >= 0 &&
                     row0 + C::BN <= p.pool_rows && p.dim == C::DPAD;
-  return fast ? base + row0 * row_bytes : nullptr;
+  return fast ? row0 * row_bytes : -1;
+}
+
+// Offsets of blocks [64 w, 64 w + 64) of a work item, one per lane (lane l:
+// block 64 w + l); the step plan reads them with readlane.
+struct BlockWindow {
+  int w;
+  int64_t off;
+};
+
+__device__ __forceinline__ int64_t readlane64(int64_t x, int lane) {
+  const u32 lo = __builtin_amdgcn_readlane((u32)x, lane);
+  const u32 hi = __builtin_amdgcn_readlane((u32)((uint64_t)x >> 32), lane);
+  return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
 template <class C, bool IS_V>
@@ -136,6 +154,12 @@ struct DmaBatch {
     }
   }
 };
+
+// Keeps the computation of x inside the scheduling region where it is
+// pinned: the empty volatile assembly reads x, so x cannot be sunk past it,
+// and volatile assembly keeps its place between the region's fences.
+__device__ __forceinline__ void pin(float x) { asm volatile("" ::"v"(x)); }
+__device__ __forceinline__ void pin(u32 x) { asm volatile("" ::"v"(x)); }
 
 // Softmax state of one wave: per 32-row group g, the exponent reference m
 // (log2 units), the row sum l and the rescale factor of the last step.
@@ -195,6 +219,7 @@ __device__ __forceinline__ void step_body(const unsigned char* ks, const unsigne
 #pragma unroll
       for (int k = 1; k < NVG; ++k) x = fmaxf(x, sc(g * NVG + k));
       mx[g] = x;
+      pin(mx[g]);
     } else if (part == G) {
       bool any = false;
 #pragma unroll
@@ -210,6 +235,7 @@ __device__ __forceinline__ void step_body(const unsigned char* ks, const unsigne
         mn[g] = st.rescale ? fmaxf(st.m[g], mx[g]) : st.m[g];
         st.alpha[g] = __builtin_amdgcn_exp2f(st.m[g] - mn[g]);
         neg_m[g] = -mn[g];
+        pin(neg_m[g]);
       }
     } else {
       const int q = part - G - 1;
@@ -222,6 +248,7 @@ __device__ __forceinline__ void step_body(const unsigned char* ks, const unsigne
           rs[g] += ev[k];
           if (kg & 1) {
             const u32 w = E::pack2(ev[k - 1], ev[k]);
+            pin(w);
             u32x4& dst = pf_cur[g][kg / 8];
             const int c = (kg % 8) / 2;
             if (c == 0) dst.x = w;
@@ -231,6 +258,8 @@ __device__ __forceinline__ void step_body(const unsigned char* ks, const unsigne
           }
         }
       }
+#pragma unroll
+      for (int g = 0; g < G; ++g) pin(rs[g]);
     }
   };
 
@@ -366,45 +395,52 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p,
 
     if (N > 0) {
       // Batch n: K block n + 3 -> K slot n % 3, V block n + 1 -> V slot (n + 1) % 3.
-      auto batch_blocks = [&](int n, int& pk, int& pv) {
-        const int jk = n + C::NSLOT < N ? n + C::NSLOT : N - 1;
-        const int jv = n + C::NSLOT - 2 < 0 ? 0 : (n + C::NSLOT - 2 < N ? n + C::NSLOT - 2 : N - 1);
-        pk = key0 + jk * C::BN;
-        pv = key0 + jv * C::BN;
-      };
-      // Plans batch n; a batch with a slow tile is issued right away.
-      auto plan_batch = [&](int n, int32_t idk, int32_t idv, DmaBatch<C>& db) {
-        int pk, pv;
-        batch_blocks(n, pk, pv);
-        db.kbase = tile_base<C, false>(p, kb, row_bytes, pk, idk, len);
-        db.vbase = tile_base<C, true>(p, vb, row_bytes, pv, idv, len);
-        db.kdst = kring_lds + (u32)(((n + C::NSLOT) % C::NSLOT) * C::TILE_BYTES);
-        db.vdst = vring_lds + (u32)(((n + 2 * C::NSLOT - 2) % C::NSLOT) * C::TILE_BYTES);
-        db.fast = db.kbase != nullptr && db.vbase != nullptr;
-        if (!db.fast) {
-          issue_slow_tile<C, false>(p, table_b, kb, row_bytes, pk, len, db.kdst, wave, lane);
-          issue_slow_tile<C, true>(p, table_b, vb, row_bytes, pv, len, db.vdst, wave, lane);
+      // Tile bases come from two 64-block windows of per-lane offsets (the V
+      // block's window and the next), refreshed when the V block leaves the
+      // first: one table read per lane every 64 steps instead of scalar
+      // page-id loads and address arithmetic on every step.
+      BlockWindow win0{0, block_offset<C>(p, table_b, row_bytes, key0, N, len, lane)};
+      BlockWindow win1{1, block_offset<C>(p, table_b, row_bytes, key0, N, len, 64 + lane)};
+      // The V block only moves forward, one block per step, and the K block
+      // is at most two blocks ahead of it: windows w(jv) and w(jv) + 1 cover both.
+      auto advance = [&](int jv) {
+        if ((jv >> 6) != win0.w) {  // uniform: the V block entered the next window
+          win0 = win1;
+          win1 = BlockWindow{win0.w + 1, block_offset<C>(p, table_b, row_bytes, key0, N, len,
+                                                         64 * (win0.w + 1) + lane)};
         }
       };
-      // Page ids of the blocks of batch n (read one step ahead of their use).
-      auto batch_ids = [&](int n, int32_t& idk, int32_t& idv) {
-        int pk, pv;
-        batch_blocks(n, pk, pv);
-        idk = page_id(p, table_b, pk);
-        idv = page_id(p, table_b, pv);
+      auto offset_of = [&](int j) {
+        return readlane64((j >> 6) == win0.w ? win0.off : win1.off, j & 63);
+      };
+      auto plan_batch = [&](int n, DmaBatch<C>& db) {
+        const int jv = n + C::NSLOT - 2 < 0 ? 0 : (n + C::NSLOT - 2 < N ? n + C::NSLOT - 2 : N - 1);
+        const int jk = n + C::NSLOT < N ? n + C::NSLOT : N - 1;
+        advance(jv);
+        const int64_t ov = offset_of(jv);
+        const int64_t ok = offset_of(jk);
+        db.kdst = kring_lds + (u32)(((n + C::NSLOT) % C::NSLOT) * C::TILE_BYTES);
+        db.vdst = vring_lds + (u32)(((n + 2 * C::NSLOT - 2) % C::NSLOT) * C::TILE_BYTES);
+        db.fast = ok >= 0 && ov >= 0;
+        db.kbase = kb + ok;
+        db.vbase = vb + ov;
+        if (!db.fast) {
+          issue_slow_tile<C, false>(p, table_b, kb, row_bytes, key0 + jk * C::BN, len, db.kdst,
+                                    wave, lane);
+          issue_slow_tile<C, true>(p, table_b, vb, row_bytes, key0 + jv * C::BN, len, db.vdst,
+                                   wave, lane);
+        }
       };
 
       DmaBatch<C> db;
-      int32_t idk, idv;
+#pragma unroll
       for (int n = -C::NSLOT; n < 0; ++n) {
-        batch_ids(n, idk, idv);
-        plan_batch(n, idk, idv, db);
+        plan_batch(n, db);
         if (db.fast) {
 #pragma unroll
-          for (int i = 0; i < C::BATCH; ++i) db.issue(i, dl, wave, row_bytes);
+          for (int q = 0; q < C::BATCH; ++q) db.issue(q, dl, wave, row_bytes);
         }
       }
-      batch_ids(0, idk, idv);
       wait_vm<2 * C::BATCH>();  // batch -3: K block 0
       __syncthreads();
 
@@ -438,8 +474,7 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p,
       auto prologue = [&](int n, f32x16(&s)[C::G][C::ST]) {
         wait_vm<C::BATCH>();  // batch n - 2: K block n + 1, V block n - 1
         __syncthreads();      // ... for every wave; the slots of step n - 1 are free
-        plan_batch(n, idk, idv, db);  // issued from inside the step body
-        batch_ids(n + 1, idk, idv);
+        plan_batch(n, db);  // issued from inside the step body
         if (st.rescale) {
 #pragma unroll
           for (int g = 0; g < C::G; ++g)

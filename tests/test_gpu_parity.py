@@ -210,3 +210,27 @@ def test_headline_shapes():
         r = check_output(got, expected, q, lengths, False, f"B{b} Q{sq} H{h} KV{kv}")
         log(f"B{b} Q{sq} H{h} KV{kv}: splits={kern.num_splits} grid={kern.compute_grid} ratio={r:.3f}")
 
+
+
+@pytest.mark.parametrize("page", [16, 64, 128])
+def test_prefill_layout_long_ragged_cache(page):
+    """The prefill layout over caches longer than its 64-block offset windows
+    (window refresh), ragged lengths, page sizes that split blocks or not, and
+    splits whose block ranges do not align with the windows."""
+    from fgw_amd.operators.mha.current import build_kernel
+    width = (8192 + page - 1) // page
+    case = (f"long_p{page}", 2, 300, 4, 128, page, width)
+    q, k, v, table = O.make_inputs(case, 2026, torch.bfloat16)
+    lengths = torch.tensor([5000, 8192], dtype=torch.int32)
+    k, v = O.poison_unread(k, v, table, lengths, page)
+    dev = [x.cuda() for x in (q, k, v, table, lengths)]
+    for causal in (False, True):
+        expected = O.chunked_reference(q, k, v, table, lengths, page, causal, 128)
+        for splits in (1, 3):
+            kern = build_kernel(2, 300, 4, 128, k.shape[0], width, page, causal, "bfloat16", 0,
+                                num_splits=None if splits == 1 else 4, layout="prefill",
+                                persistent_programs=None if splits == 1 else 5)
+            got = kern(*dev)
+            torch.cuda.synchronize()
+            check_output(got, expected, q, lengths, causal,
+                         f"prefill long page={page} causal={causal} splits={kern.num_splits}")
