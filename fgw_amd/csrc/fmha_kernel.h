@@ -417,13 +417,23 @@ __device__ __forceinline__ void mask_block(f32x16 (&s)[C::ST], int pos0, int vis
 }
 
 // Row maximum of the block, in log2 units, over the lane pair (lane, lane ^ 32).
+// Four independent chains (scores k = c mod 4; the compiler fuses pairs of
+// steps into v_max3_f32), so that one wave does not wait out the latency of
+// every step of a single chain. The maxima stay compiler-visible VALU
+// operations: the scores are read straight from MFMA accumulators, and the
+// compiler inserts the wait states that reading them requires.
 template <class C>
 __device__ __forceinline__ float row_max(const f32x16 (&s)[C::ST], float scale_log2) {
-  float mx = -INFINITY;
+  constexpr int NV = 16 * C::ST;
+  float acc[4];
 #pragma unroll
-  for (int t = 0; t < C::ST; ++t)
+  for (int c = 0; c < 4; ++c) {
+    float x = s[0][c];
 #pragma unroll
-    for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[t][v]);
+    for (int k = c + 4; k < NV; k += 4) x = fmaxf(x, s[k / 16][k % 16]);
+    acc[c] = x;
+  }
+  const float mx = fmaxf(fmaxf(acc[0], acc[1]), fmaxf(acc[2], acc[3]));
   return fmaxf(mx, __shfl_xor(mx, 32)) * scale_log2;
 }
 
@@ -450,15 +460,15 @@ __device__ __forceinline__ void softmax_pack(const f32x16 (&s)[C::ST], float m, 
   using E = Elem<C::BF16>;
   const float neg_m = -m;
   float e[C::ST][16];
-  float rs = 0.0f;
+  float rs[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // four independent partial sums
 #pragma unroll
   for (int t = 0; t < C::ST; ++t)
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
       e[t][v] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][v], scale_log2, neg_m));
-      rs += e[t][v];
+      rs[v % 4] += e[t][v];
     }
-  l += rs;
+  l += (rs[0] + rs[1]) + (rs[2] + rs[3]);
 #pragma unroll
   for (int t = 0; t < C::ST; ++t)
 #pragma unroll

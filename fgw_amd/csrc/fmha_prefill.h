@@ -1,53 +1,77 @@
 // Prefill layout of the paged attention forward (long query tiles).
 //
 // A work item is (b, h, 256-row query tile, KV split). Eight waves own 32
-// query rows each and share every K/V block (32 keys at D 128, 64 at D 64),
-// which the DMA engine
-// moves from HBM into two three-slot LDS rings (K and V). Per block the wave
-// computes S^T = K . Q^T and O^T += V^T . P^T on v_mfma_f32_32x32x16 with the
-// operand layouts of fwd_kernel (fmha_kernel.h), and the online softmax of
-// the reference (operators/mha/kernels/mha_paged_decode_ascend_v7.py:120-205).
+// query rows each and share every 64-key K/V block, which the DMA engine
+// moves from HBM into a three-slot K ring and a four-slot V ring in LDS.
+// Per block a wave computes S^T = K . Q^T and O^T += V^T . P^T on
+// v_mfma_f32_32x32x16 with the operand layouts and the online softmax of
+// fwd_kernel (fmha_kernel.h; reference math: operators/mha/kernels/
+// mha_paged_decode_ascend_v7.py:120-205).
 //
-// Software pipeline (lag 2). Step n (n = 0 .. N for N blocks) issues, in one
-// basic block:
-//   MFMA  QK^T of block n + 1 into S_next    (K ring slot (n + 1) % 3)
-//   VALU  softmax of block n: S_cur -> P_cur  (row max, exp2, row sum, pack)
-//   MFMA  PV of block n - 1 from P_prev       (V ring slot (n - 1) % 3)
-// The softmax is independent of both MFMA groups, so the matrix cores and the
-// VALU run side by side. Every step runs the same code: P of block -1 is
-// zero, the QK^T of steps N - 1 and N reads a clamped block that is never
-// used, and the softmax of step N masks every key. When block n raises the
-// exponent reference m, l is rescaled inside the softmax and O at the start
-// of step n + 1: after the PV of block n - 1 (old m), before that of block n.
+// Two wave groups, ping-pong. A workgroup of eight waves puts two waves on
+// every SIMD: wave w and wave w + 4, in groups A (waves 0-3) and B (4-7).
+// Each wave alternates a matrix phase M(n) (PV of block n - 1, then QK^T of
+// block n: MFMAs and the LDS reads that feed them) and a vector phase S(n)
+// (softmax of block n: row max, exp2, row sum, pack of P; the O rescale).
+// Group B runs one phase behind group A, and a workgroup barrier separates
+// the phases, so in every phase one wave of each SIMD issues MFMAs while
+// the other runs the softmax: the matrix cores stay busy while the VALU
+// works, which one wave alone cannot arrange (its instructions issue in
+// order).
 //
-// DMA. Batch n (planned after the barrier of step n, issued spread over the
-// step's MFMA slots) loads K block n + 3 into K slot n % 3 and V block n + 1
-// into V slot (n + 1) % 3; both slots were last read in step n - 1. Step n needs batch
-// n - 2 (K block n + 1, V block n - 1), so every load has two steps to land.
-// Batch indices outside [0, N) load a clamped block into the free slot, which
-// keeps the per-wave count of outstanding loads uniform, so the wait before
-// step n is the constant vmcnt(one batch). The loads are issued by inline
+//   phase 2m:      A: M(m)        B: S(m - 1)   all: DMA batch of block m + 2
+//   phase 2m + 1:  A: S(m)        B: M(m)       all: wait for block m + 1
+//
+// for m = 0 .. N (N blocks). M(0) runs the PV of "block -1" with P = 0 over
+// a zero-filled V slot, M(N) a QK^T of a clamped block whose scores are
+// never used, so every M phase runs the same code. S(n) rescales O after the
+// PV of block n - 1 (in M(n)) and before that of block n (in M(n + 1)).
+//
+// DMA. Block j's K and V tiles go to K slot j % 3 and V slot j % 4; the
+// batch of block j (clamped to N - 1) is issued in phase 2(j - 2) by every
+// wave (its share of the tile's 1 KB instructions). The K slot held block
+// j - 3, last read in phase 2j - 5; the V slot block j - 4, last read in
+// phase 2j - 5. The wait at the end of phase 2m + 1 leaves only the batch
+// of block m + 2 in flight, so block m + 1 (K read from phase 2m + 2) has
+// landed; V of block m was waited for a pair earlier. The pool offset of
+// block j comes from a 64-block window of per-lane offsets (one table read
+// per lane every 64 blocks) by readlane. The loads are issued by inline
 // assembly: the compiler then neither sees them as LDS writes (it would
-// otherwise wait for every outstanding DMA before each transposing LDS read)
-// nor counts them; the explicit waits here are the only ones they need, and
-// the compiler's own vmcnt waits stay correct because loads retire in order.
+// otherwise wait for every outstanding DMA before each transposing LDS
+// read) nor counts them; the explicit waits here are the only ones they
+// need, and the compiler's own vmcnt waits stay correct because loads
+// retire in order.
 #pragma once
+#include <utility>
+
 #include "fmha_kernel.h"
 
 namespace fgw_mha {
+
+// f(integral_constant<int, 0>) .. f(integral_constant<int, N - 1>) in order,
+// fully unrolled whatever the size of the body (a plain loop under
+// "#pragma unroll" may stay a loop when the body is large, and register
+// arrays indexed by its counter then move to scratch memory).
+template <class F, int... I>
+__device__ __forceinline__ void static_for_impl(F& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
 
 template <bool BF16_, int DPAD_>
 struct PCfg {
   static constexpr bool BF16 = BF16_;
   static constexpr int DPAD = DPAD_;
   static constexpr int LAYOUT = kLayoutPrefill;
-  static constexpr int NWQ = 4;  // waves along query rows; all share each K/V block
+  static constexpr int NWQ = 8;  // waves along query rows; all share each K/V block
   static constexpr int NWK = 1;
-  static constexpr int G = 2;    // 32-row groups per wave: every LDS operand feeds G MFMAs
-  static constexpr int BN = 32;  // keys per block
+  static constexpr int BN = 64;  // keys per block
   static constexpr int WAVES = NWQ;
   static constexpr int THREADS = 64 * WAVES;
-  static constexpr int ROWS_WAVE = 32 * G;
+  static constexpr int ROWS_WAVE = 32;
   static constexpr int ROWS_TILE = ROWS_WAVE * NWQ;
   static constexpr int KK = DPAD / 16;  // QK k-steps
   static constexpr int DT = DPAD / 32;  // O^T row tiles
@@ -56,11 +80,12 @@ struct PCfg {
   static constexpr int CPR = DPAD / 8;  // 16-byte chunks per LDS row
   static constexpr int ROW_BYTES = DPAD * 2;
   static constexpr int TILE_BYTES = BN * ROW_BYTES;
-  static constexpr int NSLOT = 3;
-  static constexpr int LDS_BYTES = 2 * NSLOT * TILE_BYTES;
+  static constexpr int NKSLOT = 3;
+  static constexpr int NVSLOT = 4;
+  static constexpr int LDS_BYTES = (NKSLOT + NVSLOT) * TILE_BYTES;
   static constexpr int INSTR = TILE_BYTES / 1024;  // DMA instructions per tile
   static constexpr int INSTR_PER_WAVE = INSTR / NWQ;
-  static constexpr int BATCH = 2 * INSTR_PER_WAVE;  // per wave: one K and one V tile
+  static constexpr int BATCH = 2 * INSTR_PER_WAVE;  // per wave: its share of one K and one V tile
   static constexpr int KSW = CMin<16, CPR>::value;
   static constexpr int VSW = CPR / 4;
   static constexpr int RPI = 64 / CPR;
@@ -69,13 +94,6 @@ struct PCfg {
   static_assert(LDS_BYTES <= kLdsBudget, "LDS budget of one CU");
 };
 
-// DMA of the K (IS_V false) or V tile of keys [pos0, pos0 + BN) of (b, h).
-// Instruction q of the wave fills LDS [dst + 1024 i, + 1024) with
-// i = q * NWQ + wave. Fast case: the block lies in one page, below len,
-// inside the pool, with D == DPAD; its instructions read a uniform tile base
-// plus the wave's fixed per-lane offsets (DmaBatch::issue). Otherwise every
-// key row is resolved through the table and masked chunks (key >= len,
-// d >= D, page id outside the pool) read the zero chunk (issue_slow_tile).
 // Pool byte offset (row * row_bytes) of the first key row of block j of a
 // work item (keys key0 + j BN ..), or -1 when the block needs the per-key
 // path (it straddles a page or len, leaves the pool, or D < DPAD). Blocks
@@ -96,7 +114,7 @@ __device__ __forceinline__ int64_t block_offset(const FwdParams& p, const int32_
 }
 
 // Offsets of blocks [64 w, 64 w + 64) of a work item, one per lane (lane l:
-// block 64 w + l); the step plan reads them with readlane.
+// block 64 w + l).
 struct BlockWindow {
   int w;
   int64_t off;
@@ -108,6 +126,11 @@ __device__ __forceinline__ int64_t readlane64(int64_t x, int lane) {
   return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
+// DMA of the K (IS_V false) or V tile of keys [pos0, pos0 + BN) of (b, h)
+// when the block is not in the fast case: every key row is resolved through
+// the table and masked chunks (key >= len, d >= D, page id outside the
+// pool) read the zero chunk. Instruction q of the wave fills LDS
+// [dst + 1024 i, + 1024) with i = q * NWQ + wave.
 template <class C, bool IS_V>
 __device__ __forceinline__ void issue_slow_tile(const FwdParams& p, const int32_t* table_b,
                                                 const char* base, int64_t row_bytes, int pos0,
@@ -129,176 +152,67 @@ __device__ __forceinline__ void issue_slow_tile(const FwdParams& p, const int32_
   }
 }
 
-// One batch of DMA instructions of a wave (the K tile, then the V tile) in
-// the fast case: uniform tile bases, the wave's fixed per-lane offsets and
-// uniform LDS destinations. `fast` false: the batch was issued already.
+// The wave's share of the K and V tiles of one block in the fast case (the
+// block lies in one page, below len, inside the pool, with D == DPAD):
+// uniform tile bases plus the wave's fixed per-lane offsets.
 template <class C>
-struct DmaBatch {
-  static constexpr int NI = C::BATCH;
-  bool fast;
-  const char* kbase;
-  const char* vbase;
-  u32 kdst, vdst;  // LDS byte address of the K / V slot
-  // Instruction i of the batch (K tile first); the row offset of the
-  // instruction joins the uniform base, the lane's offset is fixed.
-  __device__ __forceinline__ void issue(int i, const DmaLanes<C>& dl, int wave,
-                                        int64_t row_bytes) const {
-    constexpr int IPW = C::INSTR_PER_WAVE;
-    const int q = i % IPW;
+__device__ __forceinline__ void issue_fast_block(const char* kbase, const char* vbase, u32 kdst,
+                                                 u32 vdst, const DmaLanes<C>& dl, int wave,
+                                                 int64_t row_bytes) {
+#pragma unroll
+  for (int q = 0; q < C::INSTR_PER_WAVE; ++q) {
     const int ii = q * C::NWQ + wave;
     const int64_t rows = (int64_t)(C::RPI * ii) * row_bytes;
-    if (i < IPW) {
-      dma_saddr(kbase + rows, dl.kq(q, wave), kdst + 1024u * (u32)ii);
-    } else {
-      dma_saddr(vbase + rows, dl.vq(q, wave), vdst + 1024u * (u32)ii);
-    }
+    dma_saddr(kbase + rows, dl.kq(q, wave), kdst + 1024u * (u32)ii);
+    dma_saddr(vbase + rows, dl.vq(q, wave), vdst + 1024u * (u32)ii);
   }
-};
+}
 
-// Keeps the computation of x inside the scheduling region where it is
-// pinned: the empty volatile assembly reads x, so x cannot be sunk past it,
-// and volatile assembly keeps its place between the region's fences.
-__device__ __forceinline__ void pin(float x) { asm volatile("" ::"v"(x)); }
-__device__ __forceinline__ void pin(u32 x) { asm volatile("" ::"v"(x)); }
-
-// Softmax state of one wave: per 32-row group g, the exponent reference m
-// (log2 units), the row sum l and the rescale factor of the last step.
+// Matrix phase of one wave: O^T += V^T P^T over the V tile `vt` (the
+// previous block), then S^T = K Q^T over the K tile `kt`. One sequence of
+// DT KS + ST KK MFMAs, each operand read from LDS AH operands ahead.
 template <class C>
-struct RowState {
-  float m[C::G], l[C::G], alpha[C::G];
-  bool rescale;
-};
-
-// Body of one pipeline step, one basic block: QK^T of the next block into
-// s_next from K slot `ks`, softmax of the current block (s_cur -> pf_cur),
-// PV of the previous block from pf_prev and V slot `vs`. Sets st.rescale and
-// st.alpha when an exponent reference moved; the caller rescales O before the
-// next step's PV.
-//
-// The issue order is fixed by hand in NM slots (NM = K or V operands per
-// block): slot j issues the LDS reads of operand j + AHEAD of each product,
-// the G QK^T MFMAs of K operand j, one softmax part, the G PV MFMAs of V
-// operand j and the next softmax part; the step's DMA instructions go out
-// one per NM / BATCH slots, so that the waves of a workgroup do not queue a
-// whole batch at the same moment. Scheduling fences between slots keep each
-// read AHEAD slots before its MFMAs and the softmax spread over the MFMAs.
-// The 2 NM softmax parts: the row max of group g in part g, the new
-// references in part G, then exp2, row sum and pack of the scores.
-template <class C>
-__device__ __forceinline__ void step_body(const unsigned char* ks, const unsigned char* vs,
-                                          const DmaBatch<C>& dma, const DmaLanes<C>& dl,
-                                          int wave, int64_t row_bytes, const Lanes<C>& ln,
-                                          const u32x4 (&qf)[C::G][C::KK],
-                                          f32x16 (&s_next)[C::G][C::ST],
-                                          const f32x16 (&s_cur)[C::G][C::ST],
-                                          const u32x4 (&pf_prev)[C::G][C::KS],
-                                          u32x4 (&pf_cur)[C::G][C::KS], f32x16 (&o)[C::G][C::DT],
-                                          RowState<C>& st, float scale_log2) {
+__device__ __forceinline__ void matrix_phase(const unsigned char* kt, const unsigned char* vt,
+                                             const Lanes<C>& ln, const u32x4 (&qf)[C::KK],
+                                             const u32x4 (&pf)[C::KS], f32x16 (&s)[C::ST],
+                                             f32x16 (&o)[C::DT]) {
   using E = Elem<C::BF16>;
-  constexpr int G = C::G;
-  constexpr int NM = C::KK * C::ST;
-  static_assert(NM == C::KS * C::DT, "QK^T and PV have equal operand counts");
-  constexpr int NVG = 16 * C::ST;      // scores per lane and group
-  constexpr int NV = G * NVG;          // scores per lane
-  constexpr int NP = 2 * NM;           // softmax parts
-  constexpr int EP = NP - G - 1;       // exp2 / sum / pack parts
-  static_assert(EP >= 1, "softmax part split");
-
-  auto rk = [&](int j) { return read_k<C>(ks, ln, j % C::ST, j / C::ST); };
-  auto rv = [&](int j) { return read_vt<C>(vs, ln, j % C::DT, j / C::DT); };
-  auto sc = [&](int k) { return s_cur[k / NVG][(k % NVG) / 16][k % 16]; };
-
-  float mx[G], mn[G], neg_m[G], rs[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) rs[g] = 0.0f;
-  float ev[NV];
-  auto softmax_part = [&](int part) {
-    if (part < G) {
-      const int g = part;
-      float x = sc(g * NVG);
-#pragma unroll
-      for (int k = 1; k < NVG; ++k) x = fmaxf(x, sc(g * NVG + k));
-      mx[g] = x;
-      pin(mx[g]);
-    } else if (part == G) {
-      bool any = false;
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx[g]),
-                                                         __float_as_uint(mx[g]), false, false);
-        mx[g] = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * scale_log2;
-        any = any || mx[g] > st.m[g] + kRescaleSlack;
-      }
-      st.rescale = __ballot(any) != 0;
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        mn[g] = st.rescale ? fmaxf(st.m[g], mx[g]) : st.m[g];
-        st.alpha[g] = __builtin_amdgcn_exp2f(st.m[g] - mn[g]);
-        neg_m[g] = -mn[g];
-        pin(neg_m[g]);
-      }
-    } else {
-      const int q = part - G - 1;
-      const int k_begin = q * NV / EP, k_end = (q + 1) * NV / EP;
-#pragma unroll
-      for (int k = 0; k < NV; ++k) {
-        if (k >= k_begin && k < k_end) {
-          const int g = k / NVG, kg = k % NVG;
-          ev[k] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc(k), scale_log2, neg_m[g]));
-          rs[g] += ev[k];
-          if (kg & 1) {
-            const u32 w = E::pack2(ev[k - 1], ev[k]);
-            pin(w);
-            u32x4& dst = pf_cur[g][kg / 8];
-            const int c = (kg % 8) / 2;
-            if (c == 0) dst.x = w;
-            if (c == 1) dst.y = w;
-            if (c == 2) dst.z = w;
-            if (c == 3) dst.w = w;
-          }
-        }
-      }
-#pragma unroll
-      for (int g = 0; g < G; ++g) pin(rs[g]);
-    }
+  constexpr int NPV = C::DT * C::KS, NQK = C::ST * C::KK, NOP = NPV + NQK;
+  constexpr int AH = 7;
+  // Operand i: PV step (k2 = i / DT, dt = i % DT) for i < NPV, else QK^T step
+  // (kk = (i - NPV) / ST, t = (i - NPV) % ST).
+  auto rd = [&](auto ic) -> u32x4 {
+    constexpr int i = decltype(ic)::value;
+    if constexpr (i < NPV)
+      return read_vt<C>(vt, ln, i % C::DT, i / C::DT);
+    else
+      return read_k<C>(kt, ln, (i - NPV) % C::ST, (i - NPV) / C::ST);
   };
-
 #pragma unroll
-  for (int g = 0; g < G; ++g)
+  for (int t = 0; t < C::ST; ++t)
 #pragma unroll
-    for (int t = 0; t < C::ST; ++t)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) s_next[g][t][v] = 0.0f;
-  constexpr int AHEAD = 2;  // slots between an operand read and its MFMAs
-  u32x4 ka[AHEAD + 1], va[AHEAD + 1];
-#pragma unroll
-  for (int j = 0; j < AHEAD; ++j) {
-    ka[j] = rk(j);
-    va[j] = rv(j);
-  }
-  static_assert(NM % C::BATCH == 0, "DMA slots");
-#pragma unroll
-  for (int j = 0; j < NM; ++j) {
-    if (j % (NM / C::BATCH) == 0 && dma.fast) dma.issue(j / (NM / C::BATCH), dl, wave, row_bytes);
-    if (j + AHEAD < NM) {
-      ka[(j + AHEAD) % (AHEAD + 1)] = rk(j + AHEAD);
-      va[(j + AHEAD) % (AHEAD + 1)] = rv(j + AHEAD);
+    for (int v = 0; v < 16; ++v) s[t][v] = 0.0f;
+  u32x4 a[AH + 1];
+  // The wave of the SIMD that runs the softmax would otherwise take every
+  // VALU issue cycle it can and hold back these MFMAs; at the higher
+  // priority each MFMA issues as soon as the matrix core is free.
+  __builtin_amdgcn_s_setprio(2);
+  static_for<AH>([&](auto ic) { a[decltype(ic)::value] = rd(ic); });
+  __builtin_amdgcn_sched_barrier(0);
+  static_for<NOP>([&](auto ic) {
+    constexpr int i = decltype(ic)::value;
+    if constexpr (i + AH < NOP) a[(i + AH) % (AH + 1)] = rd(std::integral_constant<int, i + AH>{});
+    if constexpr (i < NPV) {
+      o[i % C::DT] = E::mma(a[i % (AH + 1)], pf[i / C::DT], o[i % C::DT]);
+    } else {
+      constexpr int t = (i - NPV) % C::ST, kk = (i - NPV) / C::ST;
+      s[t] = E::mma(a[i % (AH + 1)], qf[kk], s[t]);
     }
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-      s_next[g][j % C::ST] = E::mma(ka[j % (AHEAD + 1)], qf[g][j / C::ST], s_next[g][j % C::ST]);
-    softmax_part(2 * j);
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-      o[g][j % C::DT] = E::mma(va[j % (AHEAD + 1)], pf_prev[g][j / C::DT], o[g][j % C::DT]);
-    softmax_part(2 * j + 1);
+    // Fence: the machine scheduler would otherwise sink each read next to
+    // its MFMA (fewer live registers) and expose the full LDS latency.
     __builtin_amdgcn_sched_barrier(0);
-  }
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    st.m[g] = mn[g];
-    st.l[g] = st.l[g] * st.alpha[g] + rs[g];
-  }
+  });
+  __builtin_amdgcn_s_setprio(0);
 }
 
 template <class C>
@@ -307,11 +221,12 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p,
                                                              const int32_t* __restrict__ lengths) {
   __shared__ __attribute__((aligned(1024))) unsigned char smem[C::LDS_BYTES];
   unsigned char* const kring = smem;
-  unsigned char* const vring = smem + C::NSLOT * C::TILE_BYTES;
+  unsigned char* const vring = smem + C::NKSLOT * C::TILE_BYTES;
   const u32 kring_lds = lds_address(kring), vring_lds = lds_address(vring);
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool group_a = wave < C::WAVES / 2;
   const int lane = tid & 63;
   const int il = lane & 31, hh = lane >> 5;
   const Lanes<C> ln(lane);
@@ -349,183 +264,150 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p,
     const int N = blk_end - blk_begin;
     const int key0 = blk_begin * C::BN;
 
-    // Rows of this wave (group g: rows row_base + 32 g + il) and their
-    // visible key counts; blocks that end above wmin hold keys some row of
-    // the wave cannot see and are masked.
+    // Rows of this wave and their visible key counts; blocks that end above
+    // wmin hold keys some row of the wave cannot see and are masked.
     const int row_base = q0 + wave * C::ROWS_WAVE;
     int wmin = p.causal ? len - p.sq + row_base + 1 : len;
     wmin = wmin < 0 ? 0 : (wmin > len ? len : wmin);
-    int vis[C::G];
-#pragma unroll
-    for (int g = 0; g < C::G; ++g) {
-      const int qrow = row_base + 32 * g + il;
-      int v = p.causal ? len - p.sq + qrow + 1 : len;
-      vis[g] = v < 0 ? 0 : (v > len ? len : v);
-    }
+    const int qrow = row_base + il;
+    int vis = p.causal ? len - p.sq + qrow + 1 : len;
+    vis = vis < 0 ? 0 : (vis > len ? len : vis);
 
-    u32x4 qf[C::G][C::KK];
+    float m = kNegBig, l = 0.0f;
+    f32x16 o[C::DT];
 #pragma unroll
-    for (int g = 0; g < C::G; ++g) {
-      const int qrow = row_base + 32 * g + il;
-      const u16* qp =
-          static_cast<const u16*>(p.q) + (((int64_t)b * p.sq + qrow) * p.heads + h) * p.dim;
+    for (int dt = 0; dt < C::DT; ++dt)
 #pragma unroll
-      for (int kk = 0; kk < C::KK; ++kk) {
-        const int d = 16 * kk + 8 * hh;
-        u32x4 val = {0u, 0u, 0u, 0u};
-        if (qrow < p.sq && d < p.dim) val = load16(qp + d);
-        qf[g][kk] = val;
-      }
-    }
-    RowState<C> st;
-    f32x16 o[C::G][C::DT];
-#pragma unroll
-    for (int g = 0; g < C::G; ++g) {
-      st.m[g] = kNegBig;
-      st.l[g] = 0.0f;
-      st.alpha[g] = 1.0f;
-#pragma unroll
-      for (int dt = 0; dt < C::DT; ++dt)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) o[g][dt][v] = 0.0f;
-    }
-    st.rescale = false;
+      for (int v = 0; v < 16; ++v) o[dt][v] = 0.0f;
 
     __syncthreads();  // the previous work item no longer reads the rings
 
     if (N > 0) {
-      // Batch n: K block n + 3 -> K slot n % 3, V block n + 1 -> V slot (n + 1) % 3.
-      // Tile bases come from two 64-block windows of per-lane offsets (the V
-      // block's window and the next), refreshed when the V block leaves the
-      // first: one table read per lane every 64 steps instead of scalar
-      // page-id loads and address arithmetic on every step.
+      // Window of 64 block offsets holding the next batch's block; the
+      // following window is read one window ahead.
       BlockWindow win0{0, block_offset<C>(p, table_b, row_bytes, key0, N, len, lane)};
-      BlockWindow win1{1, block_offset<C>(p, table_b, row_bytes, key0, N, len, 64 + lane)};
-      // The V block only moves forward, one block per step, and the K block
-      // is at most two blocks ahead of it: windows w(jv) and w(jv) + 1 cover both.
-      auto advance = [&](int jv) {
-        if ((jv >> 6) != win0.w) {  // uniform: the V block entered the next window
+      BlockWindow win1{1, 0};
+      // K and V of block j (clamped to N - 1) into K slot j % 3, V slot j % 4.
+      auto issue_block = [&](int j) {
+        const int jc = j < N ? j : N - 1;
+        if ((jc >> 6) != win0.w) {  // uniform: the block entered the next window
           win0 = win1;
           win1 = BlockWindow{win0.w + 1, block_offset<C>(p, table_b, row_bytes, key0, N, len,
                                                          64 * (win0.w + 1) + lane)};
         }
-      };
-      auto offset_of = [&](int j) {
-        return readlane64((j >> 6) == win0.w ? win0.off : win1.off, j & 63);
-      };
-      auto plan_batch = [&](int n, DmaBatch<C>& db) {
-        const int jv = n + C::NSLOT - 2 < 0 ? 0 : (n + C::NSLOT - 2 < N ? n + C::NSLOT - 2 : N - 1);
-        const int jk = n + C::NSLOT < N ? n + C::NSLOT : N - 1;
-        advance(jv);
-        const int64_t ov = offset_of(jv);
-        const int64_t ok = offset_of(jk);
-        db.kdst = kring_lds + (u32)(((n + C::NSLOT) % C::NSLOT) * C::TILE_BYTES);
-        db.vdst = vring_lds + (u32)(((n + 2 * C::NSLOT - 2) % C::NSLOT) * C::TILE_BYTES);
-        db.fast = ok >= 0 && ov >= 0;
-        db.kbase = kb + ok;
-        db.vbase = vb + ov;
-        if (!db.fast) {
-          issue_slow_tile<C, false>(p, table_b, kb, row_bytes, key0 + jk * C::BN, len, db.kdst,
-                                    wave, lane);
-          issue_slow_tile<C, true>(p, table_b, vb, row_bytes, key0 + jv * C::BN, len, db.vdst,
-                                   wave, lane);
+        const int64_t off = readlane64(win0.off, jc & 63);
+        const u32 kdst = kring_lds + (u32)((j % C::NKSLOT) * C::TILE_BYTES);
+        const u32 vdst = vring_lds + (u32)((j % C::NVSLOT) * C::TILE_BYTES);
+        if (off >= 0) {
+          issue_fast_block<C>(kb + off, vb + off, kdst, vdst, dl, wave, row_bytes);
+        } else {
+          issue_slow_tile<C, false>(p, table_b, kb, row_bytes, key0 + jc * C::BN, len, kdst, wave,
+                                    lane);
+          issue_slow_tile<C, true>(p, table_b, vb, row_bytes, key0 + jc * C::BN, len, vdst, wave,
+                                   lane);
         }
       };
+      issue_block(0);
+      issue_block(1);
 
-      DmaBatch<C> db;
+      // Q^T operands (B of the QK^T product) load while the first blocks land.
+      u32x4 qf[C::KK];
+      {
+        const u16* qp =
+            static_cast<const u16*>(p.q) + (((int64_t)b * p.sq + qrow) * p.heads + h) * p.dim;
 #pragma unroll
-      for (int n = -C::NSLOT; n < 0; ++n) {
-        plan_batch(n, db);
-        if (db.fast) {
-#pragma unroll
-          for (int q = 0; q < C::BATCH; ++q) db.issue(q, dl, wave, row_bytes);
+        for (int kk = 0; kk < C::KK; ++kk) {
+          const int d = 16 * kk + 8 * hh;
+          u32x4 val = {0u, 0u, 0u, 0u};
+          if (qrow < p.sq && d < p.dim) val = load16(qp + d);
+          qf[kk] = val;
         }
       }
-      wait_vm<2 * C::BATCH>();  // batch -3: K block 0
+      win1.off = block_offset<C>(p, table_b, row_bytes, key0, N, len, 64 + lane);
+      // V slot 3 holds "block -1", read by the PV of M(0) with P = 0.
+      for (int i = tid * 16; i < C::TILE_BYTES; i += C::THREADS * 16)
+        *reinterpret_cast<u32x4*>(vring + (C::NVSLOT - 1) * C::TILE_BYTES + i) =
+            u32x4{0u, 0u, 0u, 0u};
+      wait_vm<C::BATCH>();  // block 0
+      // Q has landed too (its loads are younger than block 0's). The empty
+      // assembly makes the compiler wait for them here, once, instead of
+      // before the first QK^T MFMA of every matrix phase, where its vmcnt(0)
+      // would also wait for the DMA batch in flight.
+#pragma unroll
+      for (int kk = 0; kk < C::KK; ++kk) asm volatile("" ::"v"(qf[kk]));
       __syncthreads();
 
-      f32x16 s_a[C::G][C::ST], s_b[C::G][C::ST];
-      u32x4 pf_a[C::G][C::KS], pf_b[C::G][C::KS];
-      {
-        using E = Elem<C::BF16>;
+      f32x16 s[C::ST];
+      u32x4 pf[C::KS];
 #pragma unroll
-        for (int g = 0; g < C::G; ++g)
-#pragma unroll
-          for (int t = 0; t < C::ST; ++t)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) s_a[g][t][v] = 0.0f;
-#pragma unroll
-        for (int kk = 0; kk < C::KK; ++kk)
-#pragma unroll
-          for (int t = 0; t < C::ST; ++t) {
-            const u32x4 a = read_k<C>(kring, ln, t, kk);
-#pragma unroll
-            for (int g = 0; g < C::G; ++g) s_a[g][t] = E::mma(a, qf[g][kk], s_a[g][t]);
-          }
-      }
-      // P of block -1 is zero: the PV of step 0 adds nothing.
-#pragma unroll
-      for (int g = 0; g < C::G; ++g)
-#pragma unroll
-        for (int k2 = 0; k2 < C::KS; ++k2) pf_b[g][k2] = u32x4{0u, 0u, 0u, 0u};
+      for (int k2 = 0; k2 < C::KS; ++k2) pf[k2] = u32x4{0u, 0u, 0u, 0u};
 
-      // Steps n = 0 .. N; registers alternate: even steps read s_a / pf_b and
-      // write s_b / pf_a, odd steps the reverse.
-      auto prologue = [&](int n, f32x16(&s)[C::G][C::ST]) {
-        wait_vm<C::BATCH>();  // batch n - 2: K block n + 1, V block n - 1
-        __syncthreads();      // ... for every wave; the slots of step n - 1 are free
-        plan_batch(n, db);  // issued from inside the step body
-        if (st.rescale) {
-#pragma unroll
-          for (int g = 0; g < C::G; ++g)
-#pragma unroll
-            for (int dt = 0; dt < C::DT; ++dt) o[g][dt] *= st.alpha[g];
-        }
-        const int pos0 = key0 + n * C::BN;
-        if (n >= N || pos0 + C::BN > wmin) {
-#pragma unroll
-          for (int g = 0; g < C::G; ++g) mask_block<C>(s[g], pos0, n >= N ? 0 : vis[g], hh);
-        }
+      // M(n): PV of block n - 1 (V slot (n + 3) % 4), QK^T of block n (K slot n % 3).
+      auto mphase = [&](int n) {
+        matrix_phase<C>(kring + (n % C::NKSLOT) * C::TILE_BYTES,
+                        vring + ((n + C::NVSLOT - 1) % C::NVSLOT) * C::TILE_BYTES, ln, qf, pf, s,
+                        o);
       };
-      int sk = 1, sv = 2;  // ring slots of K block n + 1 and V block n - 1
-      for (int n = 0;; n += 2) {
-        prologue(n, s_a);
-        step_body<C>(kring + sk * C::TILE_BYTES, vring + sv * C::TILE_BYTES, db, dl, wave,
-                     row_bytes, ln, qf, s_b, s_a, pf_b, pf_a, o, st, p.scale_log2);
-        sk = sk == C::NSLOT - 1 ? 0 : sk + 1;
-        sv = sv == C::NSLOT - 1 ? 0 : sv + 1;
-        if (n == N) break;
-        prologue(n + 1, s_b);
-        step_body<C>(kring + sk * C::TILE_BYTES, vring + sv * C::TILE_BYTES, db, dl, wave,
-                     row_bytes, ln, qf, s_a, s_b, pf_a, pf_b, o, st, p.scale_log2);
-        sk = sk == C::NSLOT - 1 ? 0 : sk + 1;
-        sv = sv == C::NSLOT - 1 ? 0 : sv + 1;
-        if (n + 1 == N) break;
+      // S(n): softmax of block n.
+      auto sphase = [&](int n) {
+        const int pos0 = key0 + n * C::BN;
+        if (pos0 + C::BN > wmin) mask_block<C>(s, pos0, vis, hh);
+        update_ref<C>(row_max<C>(s, p.scale_log2), m, l, o);
+        softmax_pack<C>(s, m, l, p.scale_log2, pf);
+      };
+      // Group A: M(n) in phase 2n, S(n) in phase 2n + 1. Group B: S(n - 1)
+      // in phase 2n, M(n) in phase 2n + 1. Every wave issues its share of
+      // block n + 2 at the start of phase 2n and, at the end of phase
+      // 2n + 1, waits until only that batch may be in flight (block n + 1
+      // has landed). Straight-line loops per group keep the register
+      // assignment of O, S and P fixed across phases.
+      if (group_a) {
+        for (int n = 0; n < N; ++n) {
+          issue_block(n + 2);
+          mphase(n);
+          __syncthreads();
+          sphase(n);
+          wait_vm<C::BATCH>();
+          __syncthreads();
+        }
+        issue_block(N + 2);
+        mphase(N);
+        __syncthreads();
+        wait_vm<C::BATCH>();
+        __syncthreads();
+      } else {
+        issue_block(2);
+        __syncthreads();
+        mphase(0);
+        wait_vm<C::BATCH>();
+        __syncthreads();
+        for (int n = 1; n <= N; ++n) {
+          issue_block(n + 2);
+          sphase(n - 1);
+          __syncthreads();
+          mphase(n);
+          wait_vm<C::BATCH>();
+          __syncthreads();
+        }
       }
       wait_vm<0>();  // no DMA of this work item outlives it
     }
 
+    const float tot = l + __shfl_xor(l, 32);
+    if (qrow < p.sq) {
+      const float inv = 1.0f / fmaxf(tot, 1.0e-30f);
 #pragma unroll
-    for (int g = 0; g < C::G; ++g) {
-      const int qrow = row_base + 32 * g + il;
-      const float tot = st.l[g] + __shfl_xor(st.l[g], 32);
-      if (qrow < p.sq) {
-        const float inv = 1.0f / fmaxf(tot, 1.0e-30f);
+      for (int dt = 0; dt < C::DT; ++dt)
 #pragma unroll
-        for (int dt = 0; dt < C::DT; ++dt)
-#pragma unroll
-          for (int gq = 0; gq < 4; ++gq) {
-            const int d0 = 32 * dt + 8 * gq + 4 * hh;
-            if (d0 < p.dim) {
-              f32x4 val = {o[g][dt][4 * gq], o[g][dt][4 * gq + 1], o[g][dt][4 * gq + 2],
-                           o[g][dt][4 * gq + 3]};
-              store_row<C>(p, b, h, split, qrow, d0, val, inv);
-            }
+        for (int gq = 0; gq < 4; ++gq) {
+          const int d0 = 32 * dt + 8 * gq + 4 * hh;
+          if (d0 < p.dim) {
+            f32x4 val = {o[dt][4 * gq], o[dt][4 * gq + 1], o[dt][4 * gq + 2], o[dt][4 * gq + 3]};
+            store_row<C>(p, b, h, split, qrow, d0, val, inv);
           }
-        if (p.mode != 0 && hh == 0) {
-          p.lse[(((int64_t)b * p.heads + h) * p.splits + split) * p.sq + qrow] =
-              lse_of(st.m[g], tot);
         }
+      if (p.mode != 0 && hh == 0) {
+        p.lse[(((int64_t)b * p.heads + h) * p.splits + split) * p.sq + qrow] = lse_of(m, tot);
       }
     }
   }

@@ -141,11 +141,14 @@ def test_layouts_and_persistent_grids_agree():
                 got = kern(*dev)
                 torch.cuda.synchronize()
                 check_output(got, expected, q, lengths, causal, f"{layout} {persistent}")
-                outs.append((layout, got.cpu()))
+                outs.append((layout, persistent, got.cpu()))
         # Work placement never changes the arithmetic of a work item.
-        for layout, got in outs:
-            ref = next(o for lay, o in outs if lay == layout)
-            assert torch.equal(got, ref)
+        for layout, persistent, got in outs:
+            ref = next(o for lay, _, o in outs if lay == layout)
+            diff = (got.float() - ref.float()).abs()
+            assert torch.equal(got, ref), (
+                f"causal={causal} {layout} persistent={persistent}: {int((diff > 0).sum())} "
+                f"values differ, max {diff.max().item():.3g}")
 
 
 def test_partial_and_merge_components():
@@ -234,3 +237,29 @@ def test_prefill_layout_long_ragged_cache(page):
             torch.cuda.synchronize()
             check_output(got, expected, q, lengths, causal,
                          f"prefill long page={page} causal={causal} splits={kern.num_splits}")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("dim,page", [(64, 32), (96, 16), (128, 128)])
+def test_prefill_layout_dtypes_and_dims(dtype, dim, page):
+    """The prefill layout for both input dtypes, both head-dim tiles (64, 128)
+    and a padded head dim (96: every block on the per-key path), a partial
+    last query tile, ragged lengths, causal and split."""
+    from fgw_amd.operators.mha.current import build_kernel
+    width = (1500 + page - 1) // page
+    case = (f"prefill_d{dim}_p{page}", 2, 520, 2, dim, page, width)
+    q, k, v, table = O.make_inputs(case, 11, dtype)
+    lengths = torch.tensor([1500, 611], dtype=torch.int32)
+    k, v = O.poison_unread(k, v, table, lengths, page)
+    dev = [x.cuda() for x in (q, k, v, table, lengths)]
+    for causal in (False, True):
+        expected = O.reference(q, k, v, table, lengths, page, causal)
+        for splits in (None, 2):
+            kern = build_kernel(2, 520, 2, dim, k.shape[0], width, page, causal,
+                                "float16" if dtype == torch.float16 else "bfloat16", 0,
+                                num_splits=splits, layout="prefill")
+            assert kern.layout == "prefill"
+            got = kern(*dev)
+            torch.cuda.synchronize()
+            check_output(got, expected, q, lengths, causal,
+                         f"prefill d={dim} page={page} causal={causal} splits={kern.num_splits}")
