@@ -32,6 +32,10 @@ sys.path.insert(0, str(ROOT))
 
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+# Kernel of a direct (single-split) call per layout, as rocprofv3 names it.
+PREFILL_KERNELS = {"prefill": "prefill_kernel (direct, prefill layout)",
+                   "query": "fwd_kernel (direct, query layout)",
+                   "key": "fwd_kernel (direct, key layout)"}
 METRIC = "MFU% + TFLOP/s (Q4096) and µs/call + HBM GB/s (Q1 decode), 1 MI355X"
 TRAFFIC_SUMMARY = ROOT / "profiles" / "hbm_traffic_q4096_kv2048_and_q1_kv32768.md"
 COPY_PROBE_BYTES = 1 << 30
@@ -78,6 +82,25 @@ def timed_region(call, steps, warmup):
     total = marks[0].elapsed_time(marks[-1])
     per_call = [marks[2 * i].elapsed_time(marks[2 * i + 1]) for i in range(steps)]
     return total, per_call
+
+
+def region_ms(call, steps, warmup):
+    """Run `warmup` untimed calls, then exactly `steps` back-to-back calls between
+    two device synchronisations, bracketed by one pair of events on the current
+    stream (the launching stream). Returns the region's total ms. With one
+    kernel per call, total / steps is the kernel's average launch duration plus
+    the dispatch gap between launches, without per-launch event packets."""
+    import torch
+    for _ in range(warmup):
+        call()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        call()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end)
 
 
 def single_calls(call, samples):
@@ -254,10 +277,10 @@ def suite_prefill(args, emit):
     for sq in (4096, 32768):
         host = O.bench_inputs(2, sq, 8, 128, 128, 2048, torch.bfloat16)
         dinputs = [x.to(dev) for x in host]
-        for layout in (None, "prefill"):
+        for layout in ("query", "prefill"):
             kern = build_kernel(2, sq, 8, 128, host[1].shape[0], 16, 128, False, "bfloat16", 0,
                                 full_kv_cache=True, layout=layout)
-            if layout is None:
+            if layout == "query":
                 expected = O.chunked_reference(*host, 128, False, 128)
             _checked(kern, dinputs, expected, torch.bfloat16, f"prefill q{sq} {layout}")
             flops = O.useful_flops([2048] * 2, sq, 8, 128, False)
@@ -395,9 +418,9 @@ def main():
     torch.testing.assert_close(got.cpu(), expected, rtol=rtol, atol=atol)
 
     call = lambda: kern(*inputs)  # noqa: E731
-    total_ms, per_call = timed_region(call, args.steps, args.warmup)
+    total_ms = region_ms(call, args.steps, args.warmup)
     ms = total_ms / args.steps
-    kernel_ms = statistics.mean(per_call)  # direct mode: one kernel per call
+    kernel_ms = ms  # direct mode: one kernel per call
     tflops = flops / (ms * 1e-3) / 1e12
     achieved = flops / (kernel_ms * 1e-3) / 1e12
     samples = single_calls(call, args.samples)
@@ -415,7 +438,7 @@ def main():
     torch.testing.assert_close(dgot.cpu(), dexp, rtol=rtol, atol=atol)
     dbytes = O.algorithmic_bytes([dkv] * db, dsq, h, d, dkv // page)
     dcall = lambda: dkern(*dinputs)  # noqa: E731
-    d_total, _ = timed_region(dcall, args.steps, args.warmup)
+    d_total = region_ms(dcall, args.steps, args.warmup)
     d_us = statistics.median(single_calls(dcall, args.samples)) * 1e3
     decode = {"workload": "Q1/KV32768 B2H8 D128 BF16 page128", "us_per_call": d_us,
               "gbs": dbytes / (d_us * 1e-6) / 1e9,
@@ -424,8 +447,7 @@ def main():
               "grid": dkern.compute_grid, "execution_mode": dkern.execution_mode}
     if dkern.execution_mode == "split_and_merge":
         pcall = lambda: dkern.partial_kernel(*dinputs)  # noqa: E731
-        _, p_per_call = timed_region(pcall, args.steps, args.warmup)
-        p_ms = statistics.mean(p_per_call)
+        p_ms = region_ms(pcall, args.steps, args.warmup) / args.steps
         p_achieved = dbytes / (p_ms * 1e-3) / 1e9
         p_traffic = traffic_from_profile("decode_partial")
         decode["roofline"] = {"bound": "hbm", "kernel": "fwd_kernel (partial, key layout)",
@@ -448,7 +470,7 @@ def main():
                    "layout": kern.layout},
         "mfu_percent": 100.0 * tflops / PEAK_BF16_TFLOPS,
         "median_single_call_us": statistics.median(samples) * 1e3,
-        "roofline": {"bound": "mfma", "kernel": "fwd_kernel (direct, query layout)",
+        "roofline": {"bound": "mfma", "kernel": PREFILL_KERNELS[kern.layout],
                      "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / PEAK_BF16_TFLOPS,
                      "traffic": traffic_from_profile("prefill_direct"),

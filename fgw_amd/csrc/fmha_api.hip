@@ -93,10 +93,18 @@ int rows_per_tile(int layout) {
 }
 // Head-dim tiles with a prefill-layout kernel.
 bool has_prefill(int dpad) { return dpad == 64 || dpad == 128; }
-// The automatic layout choice uses the prefill layout only when asked for
-// explicitly; it is not yet faster than the query layout on MI355X.
-constexpr bool kAutoPrefill = false;
-constexpr int kPrefillMinSq = 129;
+// The automatic layout choice takes the prefill layout when its 256-row
+// query tiles alone give every resident program of the device a work item:
+// measured on MI355X it is then faster than the query layout (B2 H8 D128
+// BF16, KV 2048: Q 4096 and Q 32768). Fewer tiles leave compute units idle,
+// where the query layout's 128-row tiles and KV splits fill the device.
+bool auto_prefill(const fgw_mha_shape* s, const fgw_mha_device_info* dev, int dpad) {
+  if (!has_prefill(dpad) || s->sq < 256) return false;
+  const int rows = 256;
+  const int64_t tiles = (int64_t)s->batch * s->heads * ((s->sq + rows - 1) / rows);
+  const int wg = dev->wg_per_cu[kLayoutPrefill] > 0 ? dev->wg_per_cu[kLayoutPrefill] : 1;
+  return tiles >= (int64_t)dev->num_cus * wg;
+}
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
@@ -254,9 +262,7 @@ int fgw_mha_plan(const fgw_mha_shape* s, const fgw_mha_request* req,
   int layout = req->layout;
   if (layout == FGW_MHA_LAYOUT_AUTO) {
     layout = s->sq <= 32 ? kLayoutKey
-                         : (kAutoPrefill && s->sq >= kPrefillMinSq && has_prefill(dpad)
-                                ? kLayoutPrefill
-                                : kLayoutQuery);
+                         : (auto_prefill(s, dev, dpad) ? kLayoutPrefill : kLayoutQuery);
   }
   if (layout != kLayoutQuery && layout != kLayoutKey && layout != kLayoutPrefill)
     return fail(FGW_MHA_EINVAL, "layout must be -1 (auto), 0 (query), 1 (key) or 2 (prefill)");

@@ -416,6 +416,19 @@ __device__ __forceinline__ void mask_block(f32x16 (&s)[C::ST], int pos0, int vis
     }
 }
 
+// max / sum of x over the lane pair (lane, lane ^ 32) by v_permlane32_swap:
+// a VALU exchange of the wave's halves, where a lane shuffle would go
+// through the LDS crossbar and queue behind the operand reads of the wave
+// that shares the SIMD. Both lanes of a pair get bit-identical results.
+__device__ __forceinline__ float pair_max(float x) {
+  const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+}
+__device__ __forceinline__ float pair_sum(float x) {
+  const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+}
+
 // Row maximum of the block, in log2 units, over the lane pair (lane, lane ^ 32).
 // Four independent chains (scores k = c mod 4; the compiler fuses pairs of
 // steps into v_max3_f32), so that one wave does not wait out the latency of
@@ -434,7 +447,7 @@ __device__ __forceinline__ float row_max(const f32x16 (&s)[C::ST], float scale_l
     acc[c] = x;
   }
   const float mx = fmaxf(fmaxf(acc[0], acc[1]), fmaxf(acc[2], acc[3]));
-  return fmaxf(mx, __shfl_xor(mx, 32)) * scale_log2;
+  return pair_max(mx) * scale_log2;
 }
 
 // The exponent reference m moves only when a row maximum of the wave exceeds
@@ -647,7 +660,7 @@ __global__ __launch_bounds__(C::THREADS) void fwd_kernel(FwdParams p,
 
     wait_dma();  // no DMA of this work item outlives it
     if constexpr (C::NWK == 1) {
-      const float tot = l + __shfl_xor(l, 32);
+      const float tot = pair_sum(l);
       if (qrow < p.sq) {
         const float inv = 1.0f / fmaxf(tot, 1.0e-30f);
 #pragma unroll
@@ -670,7 +683,7 @@ __global__ __launch_bounds__(C::THREADS) void fwd_kernel(FwdParams p,
       float* cm = reinterpret_cast<float*>(smem);
       float* cl = cm + C::NWK * C::ROWS_WAVE;
       float* co = cl + C::NWK * C::ROWS_WAVE;
-      const float tot = l + __shfl_xor(l, 32);
+      const float tot = pair_sum(l);
       if (hh == 0) {
         cm[wk * C::ROWS_WAVE + il] = m;
         cl[wk * C::ROWS_WAVE + il] = tot;

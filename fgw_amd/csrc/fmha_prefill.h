@@ -393,7 +393,7 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p,
       wait_vm<0>();  // no DMA of this work item outlives it
     }
 
-    const float tot = l + __shfl_xor(l, 32);
+    const float tot = pair_sum(l);
     if (qrow < p.sq) {
       const float inv = 1.0f / fmaxf(tot, 1.0e-30f);
 #pragma unroll

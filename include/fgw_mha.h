@@ -53,7 +53,8 @@ typedef enum {
   FGW_MHA_LAYOUT_AUTO = -1,
   FGW_MHA_LAYOUT_QUERY = 0, /* 4 waves x 32 query rows share 64-key K/V tiles (prefill) */
   FGW_MHA_LAYOUT_KEY = 1,   /* 4 waves split the keys of 32 query rows (decode) */
-  FGW_MHA_LAYOUT_PREFILL = 2 /* 8 waves x 32 query rows, pipelined K/V rings; D in (32, 128] */
+  FGW_MHA_LAYOUT_PREFILL = 2 /* 8 waves x 32 query rows in two groups that alternate MFMA and
+                                softmax phases over shared 64-key K/V rings; D in (32, 128] */
 } fgw_mha_layout;
 
 #define FGW_MHA_NUM_LAYOUTS 3

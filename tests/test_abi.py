@@ -42,12 +42,16 @@ def shape(b=2, sq=1, h=8, d=128, kv=32768, page=128, causal=0, dtype=_lib.DTYPE_
 
 
 def test_plan_headline_shapes(lib):
+    # 2 x 8 x 16 prefill tiles of 256 rows fill the 256 CUs: prefill layout.
     prefill = _lib.plan(shape(sq=4096, kv=2048), _lib.Request(0, -1, -1), DEVICE)
-    assert (prefill.layout, prefill.rows_per_tile, prefill.q_tiles, prefill.num_splits) == (0, 128, 32, 1)
-    assert (prefill.work_items, prefill.grid, prefill.execution_mode) == (512, 512, 0)
-    assert prefill.threads == 256
+    assert (prefill.layout, prefill.rows_per_tile, prefill.q_tiles, prefill.num_splits) == (2, 256, 16, 1)
+    assert (prefill.work_items, prefill.grid, prefill.execution_mode) == (256, 256, 0)
+    assert prefill.threads == 512
     mid = _lib.plan(shape(sq=128, kv=2048), _lib.Request(0, -1, -1), DEVICE)
-    assert (mid.layout, mid.rows_per_tile) == (0, 128)  # up to 128 queries: query layout
+    assert (mid.layout, mid.rows_per_tile, mid.threads) == (0, 128, 256)  # short Q: query layout
+    # 64 prefill tiles would leave CUs idle: query layout (128-row tiles, KV splits).
+    few = _lib.plan(shape(sq=1024, kv=2048), _lib.Request(0, -1, -1), DEVICE)
+    assert few.layout == 0
     wide = _lib.plan(shape(sq=4096, kv=2048, d=256), _lib.Request(0, -1, -1), DEVICE)
     assert (wide.layout, wide.dim_padded) == (0, 256)  # no prefill kernel for D > 128
     narrow = _lib.plan(shape(sq=4096, kv=2048, d=32), _lib.Request(0, -1, -1), DEVICE)
@@ -56,7 +60,8 @@ def test_plan_headline_shapes(lib):
     assert (decode.layout, decode.rows_per_tile, decode.num_splits, decode.work_items) == (1, 32, 32, 512)
     assert decode.parts_floats == 2 * 8 * 32 * 1 * 128 and decode.lse_floats == 2 * 8 * 32
     big = _lib.plan(shape(sq=32768, kv=2048), _lib.Request(0, -1, -1), DEVICE)
-    assert big.work_items == 2 * 8 * 256 and big.grid == 512  # persistent cap = 256 CUs x 2
+    assert big.layout == 2 and big.work_items == 2 * 8 * 128
+    assert big.grid == 256  # persistent cap = 256 CUs x 1 program
     uncapped = _lib.plan(shape(sq=32768, kv=2048), _lib.Request(0, 0, -1), DEVICE)
     assert uncapped.grid == uncapped.work_items
     capped = _lib.plan(shape(sq=32768, kv=2048), _lib.Request(0, 28, -1), DEVICE)
