@@ -10,7 +10,9 @@
 //   s = q.k * D^-0.5, running max m, p = exp(s - m) rounded to the input dtype
 //   for the PV product, l = l*alpha + sum(p) in fp32, O = alpha*O + P.V,
 //   output O / max(l, 1e-30); partial mode stores O/l and LSE = ln(l) + m.
-// The exponentials run as exp2 on log2(e)-prescaled scores. The head dim is
+// The exponentials run as exp2 on log2(e)-prescaled scores, against an
+// exponent reference m that moves only when a block's row sums leave a bound
+// (online_softmax): mathematically the same O/l and LSE. The head dim is
 // padded with zeros to a power of two >= 32 (as cube_general.py:31 does);
 // the scale uses the true D.
 //
@@ -31,9 +33,9 @@
 //                   S^T accumulator after the softmax: the 16 keys a lane
 //                   holds are its B-operand k-slots once the A operand reads
 //                   keys (16ks + 4*(lane/32) + 0..3) and (... + 8 + 0..3).
-// Every lane owns one query row in both products: the softmax needs one
-// cross-half (lane ^ 32) exchange per block for the max, and the rescale of O
-// is lane-local.
+// Every lane owns one query row in both products: the row maximum (taken only
+// when the exponent reference moves) needs one cross-half (lane ^ 32)
+// exchange, and the rescale of O is lane-local.
 //
 // Layouts (template parameter LAYOUT):
 //   kLayoutQuery: 4 waves x 32 query rows share each 64-key K/V tile in
@@ -68,7 +70,7 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kNegBig = -1.0e30f;  // running-max floor and empty-split LSE
-constexpr float kRescaleSlack = 8.0f;  // log2 headroom of p before O/l are rescaled
+constexpr float kSoftmaxSumBound = 8192.0f;  // lane row-sum bound before O/l are rescaled
 constexpr int kNumXcd = 8;
 constexpr int kLdsBudget = 160 * 1024;
 
@@ -450,38 +452,23 @@ __device__ __forceinline__ float row_max(const f32x16 (&s)[C::ST], float scale_l
   return pair_max(mx) * scale_log2;
 }
 
-// The exponent reference m moves only when a row maximum of the wave exceeds
-// it by more than kRescaleSlack (log2 units): p stays <= 2^kRescaleSlack and
-// the O/l rescale runs on few blocks. O/l and the LSE do not depend on m.
+// p = exp2(s * scale_log2 - m) packed to the input dtype as the B operands of
+// the PV product (k-step 2 t + u = s[t][8 u .. 8 u + 7]); returns the lane's
+// part of the row sum (fp32, four independent partial sums).
 template <class C>
-__device__ __forceinline__ void update_ref(float mx, float& m, float& l, f32x16 (&o)[C::DT]) {
-  if (__ballot(mx > m + kRescaleSlack)) {
-    const float mn = fmaxf(m, mx);
-    const float alpha = __builtin_amdgcn_exp2f(m - mn);
-    l *= alpha;
-#pragma unroll
-    for (int dt = 0; dt < C::DT; ++dt) o[dt] *= alpha;
-    m = mn;
-  }
-}
-
-// p = exp2(s * scale_log2 - m), l += sum(p) in fp32, P packed to the input
-// dtype as the B operands of the PV product (k-step 2 t + u = s[t][8 u .. 8 u + 7]).
-template <class C>
-__device__ __forceinline__ void softmax_pack(const f32x16 (&s)[C::ST], float m, float& l,
-                                             float scale_log2, u32x4 (&pf)[C::KS]) {
+__device__ __forceinline__ float softmax_exp(const f32x16 (&s)[C::ST], float m, float scale_log2,
+                                             u32x4 (&pf)[C::KS]) {
   using E = Elem<C::BF16>;
   const float neg_m = -m;
   float e[C::ST][16];
-  float rs[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // four independent partial sums
+  float rs[4];
 #pragma unroll
   for (int t = 0; t < C::ST; ++t)
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
       e[t][v] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][v], scale_log2, neg_m));
-      rs[v % 4] += e[t][v];
+      rs[v % 4] = t == 0 && v < 4 ? e[t][v] : rs[v % 4] + e[t][v];
     }
-  l += (rs[0] + rs[1]) + (rs[2] + rs[3]);
 #pragma unroll
   for (int t = 0; t < C::ST; ++t)
 #pragma unroll
@@ -493,6 +480,32 @@ __device__ __forceinline__ void softmax_pack(const f32x16 (&s)[C::ST], float m, 
       w.w = E::pack2(e[t][8 * u + 6], e[t][8 * u + 7]);
       pf[2 * t + u] = w;
     }
+  return (rs[0] + rs[1]) + (rs[2] + rs[3]);
+}
+
+// Online softmax of one block: P against the current exponent reference m,
+// l += row sum. The reference m moves (to the block's row maximum, with O and
+// l rescaled and P recomputed) only when some lane's sum exceeds
+// kSoftmaxSumBound: on the first block of a row (m = -1e30) and when a block
+// raises the maximum by about 8 (log2 units) or more. Otherwise no row
+// maximum is taken at all. Every p <= sum <= kSoftmaxSumBound, within FP16's
+// range; O/l and the LSE do not depend on m, and m never exceeds the running
+// maximum, so no p underflows earlier than with m at the running maximum.
+template <class C>
+__device__ __forceinline__ void online_softmax(const f32x16 (&s)[C::ST], float& m, float& l,
+                                               f32x16 (&o)[C::DT], float scale_log2,
+                                               u32x4 (&pf)[C::KS]) {
+  float rs = softmax_exp<C>(s, m, scale_log2, pf);
+  if (__ballot(!(rs <= kSoftmaxSumBound))) {
+    const float mn = fmaxf(m, row_max<C>(s, scale_log2));
+    const float alpha = __builtin_amdgcn_exp2f(m - mn);
+    l *= alpha;
+#pragma unroll
+    for (int dt = 0; dt < C::DT; ++dt) o[dt] *= alpha;
+    m = mn;
+    rs = softmax_exp<C>(s, m, scale_log2, pf);
+  }
+  l += rs;
 }
 
 // O^T += V^T P^T for one block, V^T operands read one step ahead.
@@ -646,8 +659,7 @@ __global__ __launch_bounds__(C::THREADS) void fwd_kernel(FwdParams p,
       u32x4 pf[C::KS];
       qk_block<C>(stage, ln, qf, s);
       if (pos0 + C::BN > wmin) mask_block<C>(s, pos0, vis, hh);
-      update_ref<C>(row_max<C>(s, p.scale_log2), m, l, o);
-      softmax_pack<C>(s, m, l, p.scale_log2, pf);
+      online_softmax<C>(s, m, l, o, p.scale_log2, pf);
       pv_block<C>(stage + C::TILE_BYTES, ln, pf, o);
       if (n + 1 < my_n && C::NBUF == 1) {
         group_sync<C>();  // single stage: refill only after every wave has read it

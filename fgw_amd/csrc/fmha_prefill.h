@@ -12,7 +12,8 @@
 // every SIMD: wave w and wave w + 4, in groups A (waves 0-3) and B (4-7).
 // Each wave alternates a matrix phase M(n) (PV of block n - 1, then QK^T of
 // block n: MFMAs and the LDS reads that feed them) and a vector phase S(n)
-// (softmax of block n: row max, exp2, row sum, pack of P; the O rescale).
+// (softmax of block n: exp2, row sum, pack of P; the row max and the O
+// rescale only when the exponent reference has to move).
 // Group B runs one phase behind group A, and a workgroup barrier separates
 // the phases, so in every phase one wave of each SIMD issues MFMAs while
 // the other runs the softmax: the matrix cores stay busy while the VALU
@@ -352,8 +353,7 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p,
       auto sphase = [&](int n) {
         const int pos0 = key0 + n * C::BN;
         if (pos0 + C::BN > wmin) mask_block<C>(s, pos0, vis, hh);
-        update_ref<C>(row_max<C>(s, p.scale_log2), m, l, o);
-        softmax_pack<C>(s, m, l, p.scale_log2, pf);
+        online_softmax<C>(s, m, l, o, p.scale_log2, pf);
       };
       // Group A: M(n) in phase 2n, S(n) in phase 2n + 1. Group B: S(n - 1)
       // in phase 2n, M(n) in phase 2n + 1. Every wave issues its share of

@@ -263,3 +263,33 @@ def test_prefill_layout_dtypes_and_dims(dtype, dim, page):
             torch.cuda.synchronize()
             check_output(got, expected, q, lengths, causal,
                          f"prefill d={dim} page={page} causal={causal} splits={kern.num_splits}")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("rise", [48.0, 96.0])
+def test_rising_scores_move_the_exponent_reference(dtype, rise):
+    """Scores that rise along the keys make every 64-key block raise the row
+    maximum by about 10 (rise 48: p up to ~2^10 against the previous exponent
+    reference, under the sum bound) or about 20 log2 units (rise 96: the
+    rescale path -- row maximum, O/l rescale, P recomputed -- runs on every
+    block), in every layout."""
+    from fgw_amd.operators.mha.current import build_kernel
+    page, width, sq = 64, 24, 300
+    case = ("rising", 2, sq, 2, 128, page, width)
+    q, k, v, table = O.make_inputs(case, 5, dtype)
+    q = (q.float().abs() * 0.5 + 0.25).to(dtype)  # positive queries
+    ramp = torch.linspace(0.0, rise, k.shape[0])[:, None, None]
+    k = (k.float().abs() * 0.1 + ramp).to(dtype)  # pool row r: scores grow with r
+    # Table pages in pool order, so scores rise with the key position too.
+    table = torch.arange(2 * width, dtype=torch.int32).reshape(2, width)
+    lengths = torch.tensor([1500, 977], dtype=torch.int32)
+    dev = [x.cuda() for x in (q, k, v, table, lengths)]
+    for causal in (False, True):
+        expected = O.reference(q, k, v, table, lengths, page, causal)
+        for layout in ("query", "key", "prefill"):
+            kern = build_kernel(2, sq, 2, 128, k.shape[0], width, page, causal,
+                                "float16" if dtype == torch.float16 else "bfloat16", 0,
+                                layout=layout)
+            got = kern(*dev)
+            torch.cuda.synchronize()
+            check_output(got, expected, q, lengths, causal, f"rising {layout} causal={causal}")
