@@ -62,6 +62,8 @@ SIGNATURES = {
                       c_void_p),
     "fgw_mha_gather_kv": (ctypes.POINTER(Shape), ctypes.POINTER(Tensors), c_void_p, c_void_p,
                           c_int32, c_void_p),
+    "fgw_mha_pack_pages": (ctypes.POINTER(Shape), ctypes.POINTER(Tensors), c_void_p, c_int32,
+                           c_void_p, c_void_p, c_void_p),
 }
 
 _lock = threading.Lock()

@@ -61,6 +61,12 @@ hipError_t launch_gather(const GatherParams& p, hipStream_t stream) {
   return hipGetLastError();
 }
 
+hipError_t launch_pack(const PackParams& p, int total_pages, hipStream_t stream) {
+  const int64_t wgs = (int64_t)total_pages * p.wg_per_page;
+  pack_pages_kernel<<<dim3((unsigned)wgs), dim3(kPackThreads), 0, stream>>>(p);
+  return hipGetLastError();
+}
+
 }  // namespace fgw_mha
 
 using namespace fgw_mha;
@@ -381,6 +387,40 @@ int fgw_mha_gather_kv(const fgw_mha_shape* s, const fgw_mha_tensors* t, void* ou
   page_divisor((uint32_t)s->page_size, &g.page_magic, &g.page_shift);
   const hipError_t err = launch_gather(g, stream);
   return err == hipSuccess ? FGW_MHA_OK : hip_fail(err, "gather kernel launch");
+}
+
+int fgw_mha_pack_pages(const fgw_mha_shape* s, const fgw_mha_tensors* t, const int32_t* cu_rows,
+                       int32_t total_pages, void* out_k, void* out_v, hipStream_t stream) {
+  int rc = check_shape(s);
+  if (rc) return rc;
+  if (!t || !t->k_cache || !t->v_cache || !t->block_table || !cu_rows || !out_k || !out_v)
+    return fail(FGW_MHA_EINVAL, "pack needs K/V, table, cu_rows and two outputs");
+  if (!aligned16(t->k_cache) || !aligned16(t->v_cache) || !aligned16(out_k) || !aligned16(out_v))
+    return fail(FGW_MHA_EINVAL, "pack buffers must be 16-byte aligned");
+  if (total_pages < 0) return fail(FGW_MHA_EINVAL, "total_pages must not be negative");
+  const int64_t page_bytes = (int64_t)s->page_size * s->heads * s->dim * 2;
+  if (page_bytes % 16) return fail(FGW_MHA_EINVAL, "a page must hold whole 16-byte chunks");
+  const int64_t page_chunks = page_bytes / 16;
+  const int64_t wpp = (page_chunks + kPackChunks - 1) / kPackChunks;
+  if (page_chunks > INT32_MAX || (int64_t)total_pages * wpp > INT32_MAX ||
+      (int64_t)total_pages * s->page_size > INT32_MAX)
+    return fail(FGW_MHA_EUNSUPPORTED, "packed cache exceeds 2^31 rows or workgroups");
+  if (total_pages == 0) return FGW_MHA_OK;
+  PackParams p;
+  p.k = t->k_cache;
+  p.v = t->v_cache;
+  p.table = t->block_table;
+  p.cu_rows = cu_rows;
+  p.out_k = out_k;
+  p.out_v = out_v;
+  p.pool_rows = s->pool_rows;
+  p.batch = s->batch;
+  p.width = s->width;
+  p.page_size = s->page_size;
+  p.page_chunks = (int32_t)page_chunks;
+  p.wg_per_page = (int32_t)wpp;
+  const hipError_t err = launch_pack(p, total_pages, stream);
+  return err == hipSuccess ? FGW_MHA_OK : hip_fail(err, "pack kernel launch");
 }
 
 }  // extern "C"

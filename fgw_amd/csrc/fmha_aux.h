@@ -109,4 +109,62 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherParams p) {
   }
 }
 
+// Page-granular packing of the live cache: packed page g (rows
+// [g page, g page + page) of out) is page j of request b, where b is the
+// request whose packed rows [cu_rows[b], cu_rows[b + 1]) hold row g page and
+// j = (g page - cu_rows[b]) / page; its source is pool page table[b, j],
+// copied whole (rows past len included), or zeros for a page id outside the
+// pool. The format is the reference's packed cache
+// (benchmarks/mha/external_cache_gather.py:28-35: each request's live
+// region rounded up to whole pages, in request order). One workgroup moves
+// kPackChunks 16-byte chunks of K and of V of one page; every thread issues
+// all its loads before its stores.
+constexpr int kPackThreads = 256;
+constexpr int kPackPerThread = 4;
+constexpr int kPackChunks = kPackThreads * kPackPerThread;
+__global__ __launch_bounds__(kPackThreads) void pack_pages_kernel(PackParams p) {
+  const int g = (int)(blockIdx.x / (unsigned)p.wg_per_page);
+  const int part = (int)(blockIdx.x % (unsigned)p.wg_per_page);
+  const int64_t row0 = (int64_t)g * p.page_size;
+  // Request b: the last b with cu_rows[b] <= row0 (empty requests have
+  // cu_rows[b] == cu_rows[b + 1] and are passed over).
+  int lo = 0, hi = p.batch;  // cu_rows[lo] <= row0 < cu_rows[hi]
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (p.cu_rows[mid] <= row0) lo = mid; else hi = mid;
+  }
+  const int b = lo;
+  const int64_t j = (row0 - p.cu_rows[b]) / p.page_size;
+  int64_t src_page = -1;
+  if (j >= 0 && j < p.width) {
+    const int32_t id = p.table[(int64_t)b * p.width + j];
+    if (id >= 0 && ((int64_t)id + 1) * p.page_size <= p.pool_rows) src_page = id;
+  }
+  const int64_t src = src_page >= 0 ? src_page * p.page_chunks : 0;
+  const u32x4* ks = static_cast<const u32x4*>(p.k) + src;
+  const u32x4* vs = static_cast<const u32x4*>(p.v) + src;
+  u32x4* ko = static_cast<u32x4*>(p.out_k) + (int64_t)g * p.page_chunks;
+  u32x4* vo = static_cast<u32x4*>(p.out_v) + (int64_t)g * p.page_chunks;
+  const int c0 = part * kPackChunks + (int)threadIdx.x;
+  u32x4 kx[kPackPerThread], vx[kPackPerThread];
+#pragma unroll
+  for (int i = 0; i < kPackPerThread; ++i) {
+    const int c = c0 + i * kPackThreads;
+    kx[i] = u32x4{0u, 0u, 0u, 0u};
+    vx[i] = u32x4{0u, 0u, 0u, 0u};
+    if (src_page >= 0 && c < p.page_chunks) {
+      kx[i] = ks[c];
+      vx[i] = vs[c];
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kPackPerThread; ++i) {
+    const int c = c0 + i * kPackThreads;
+    if (c < p.page_chunks) {
+      ko[c] = kx[i];
+      vo[c] = vx[i];
+    }
+  }
+}
+
 }  // namespace fgw_mha

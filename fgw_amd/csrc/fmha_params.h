@@ -52,4 +52,18 @@ struct GatherParams {
   uint32_t page_magic, page_shift;
 };
 
+// Page-granular packing of the live cache (see pack_pages_kernel).
+struct PackParams {
+  const void* k;
+  const void* v;
+  const int32_t* table;
+  const int32_t* cu_rows;  // [B + 1] packed row offsets, multiples of page_size
+  void* out_k;             // [cu_rows[B], H, D]
+  void* out_v;
+  int64_t pool_rows;
+  int32_t batch, width, page_size;
+  int32_t page_chunks;  // 16-byte chunks of one page (page_size * H * D * 2 / 16)
+  int32_t wg_per_page;
+};
+
 }  // namespace fgw_mha

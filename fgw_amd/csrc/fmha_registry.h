@@ -25,6 +25,7 @@ inline int dim_tile(int dim) {
 FwdEntry fwd_entry(bool bf16, int dpad, int layout);
 hipError_t launch_merge(bool bf16, const MergeParams& p, hipStream_t stream);
 hipError_t launch_gather(const GatherParams& p, hipStream_t stream);
+hipError_t launch_pack(const PackParams& p, int total_pages, hipStream_t stream);
 
 }  // namespace fgw_mha
 

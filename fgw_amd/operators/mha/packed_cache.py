@@ -1,0 +1,160 @@
+"""Packed K/V cache: every request's live pages, contiguous, and attention over it.
+
+The reference's packed-cache path (benchmarks/mha/external_cache_gather.py:
+14-77) rounds each request's live region up to whole pages, copies those
+pages in request order into a dense cache with a TileOPs paged-cache gather
+(one call for K, one for V), checks the copy row-exactly, and runs its paged
+attention over the dense cache through an identity page table. Here the copy
+is one launch of fgw_mha_pack_pages (K and V together, whole pages, zero pages
+for ids outside the pool) and the attention is build_kernel's.
+
+pack_paged_cache is the format step on its own; build_gather_attention keeps
+the reference helper's arguments and returns the same (callable, info) pair.
+"""
+from __future__ import annotations
+
+import ctypes
+from collections import namedtuple
+from typing import Sequence
+
+import torch
+
+from fgw_amd import _lib
+from fgw_amd.operators.mha.kernels.mha_paged_decode_hip import _current_stream
+
+PackedCache = namedtuple("PackedCache", "k v table cu_rows offsets rows")
+
+
+def packed_layout(lengths: Sequence[int], page_size: int, width: int):
+    """(offsets, rows, table rows) of the packed cache (external_cache_gather.py:28-35):
+    offsets[i + 1] - offsets[i] = ceil(len_i / page) * page; rows = max(page, total);
+    table row i maps page j to offsets[i] // page + j."""
+    offsets = [0]
+    for n in lengths:
+        offsets.append(offsets[-1] + -(-int(n) // page_size) * page_size)
+    rows = max(page_size, offsets[-1])
+    table = [[offsets[i] // page_size + j for j in range(width)] for i in range(len(lengths))]
+    return offsets, rows, table
+
+
+def _host_lengths(lengths, batch, capacity):
+    if isinstance(lengths, torch.Tensor):
+        if lengths.device.type != "cpu":
+            raise ValueError("pack needs host-known lengths (a sequence or a CPU tensor)")
+        lengths = lengths.tolist()
+    lengths = [int(n) for n in lengths]
+    if len(lengths) != batch:
+        raise ValueError("metadata shape mismatch")
+    if any(n < 0 or n > capacity for n in lengths):
+        raise ValueError("Cache lengths must be within table capacity")
+    return lengths
+
+
+def _check_cache(k_cache, v_cache, block_table, page_size):
+    if k_cache.ndim != 3 or v_cache.shape != k_cache.shape:
+        raise ValueError("K/V shape mismatch")
+    if k_cache.dtype not in (torch.float16, torch.bfloat16) or v_cache.dtype != k_cache.dtype:
+        raise ValueError("matching FP16/BF16 Q/K/V required")
+    if block_table.ndim != 2 or block_table.shape[1] <= 0 or block_table.dtype != torch.int32:
+        raise ValueError("int32 metadata required")
+    if page_size <= 0 or k_cache.shape[0] <= 0 or k_cache.shape[0] % page_size:
+        raise ValueError("positive page size, whole pool pages and positive table width required")
+    if k_cache.device.type != "cuda" or any(x.device != k_cache.device or not x.is_contiguous()
+                                            for x in (k_cache, v_cache, block_table)):
+        raise ValueError("contiguous inputs on the same GPU required")
+
+
+def _launch_pack(k_cache, v_cache, block_table, cu_rows, total_pages, page_size, out_k, out_v):
+    n, h, d = k_cache.shape
+    b, w = block_table.shape
+    shape = _lib.Shape(b, 1, h, d, n, w, page_size, 0,
+                       _lib.DTYPE_BFLOAT16 if k_cache.dtype == torch.bfloat16
+                       else _lib.DTYPE_FLOAT16)
+    t = _lib.Tensors(None, k_cache.data_ptr(), v_cache.data_ptr(), block_table.data_ptr(),
+                     None, None, None, None)
+    lib = _lib.load()
+    _lib.check(lib.fgw_mha_pack_pages(ctypes.byref(shape), ctypes.byref(t), cu_rows.data_ptr(),
+                                      total_pages, out_k.data_ptr(), out_v.data_ptr(),
+                                      _current_stream(k_cache.device.index)))
+
+
+def pack_paged_cache(k_cache, v_cache, block_table, lengths, page_size) -> PackedCache:
+    """Copy every request's live pages, whole and in order, into a dense cache.
+
+    `lengths` are host-known (a sequence or a CPU tensor), as in the
+    reference helper, which computes the offsets on the host. Returns the
+    dense K/V [rows, H, D], the identity page table [B, W] (int32, device),
+    the row offsets (int32 [B + 1], device, and as a host list) and rows.
+    Rows past the last packed page (only when every length is 0) are zero.
+    """
+    _check_cache(k_cache, v_cache, block_table, page_size)
+    b, w = block_table.shape
+    lengths = _host_lengths(lengths, b, w * page_size)
+    offsets, rows, table = packed_layout(lengths, page_size, w)
+    dev = k_cache.device
+    cu_rows = torch.tensor(offsets, dtype=torch.int32, device=dev)
+    dense_table = torch.tensor(table, dtype=torch.int32, device=dev)
+    h, d = k_cache.shape[1:]
+    out_k = torch.empty((rows, h, d), dtype=k_cache.dtype, device=dev)
+    out_v = torch.empty_like(out_k)
+    if offsets[-1] < rows:
+        out_k[offsets[-1]:].zero_()
+        out_v[offsets[-1]:].zero_()
+    _launch_pack(k_cache, v_cache, block_table, cu_rows, offsets[-1] // page_size, page_size,
+                 out_k, out_v)
+    return PackedCache(out_k, out_v, dense_table, cu_rows, offsets, rows)
+
+
+def build_gather_attention(case, dtype_name, inputs, cube, splits, device_index):
+    """Pack, check the packed rows exactly, and build attention over the packed cache.
+
+    Arguments as in external_cache_gather.py:14: case = (name, B, Sq, H, D,
+    page, width, lengths, causal) with host lengths, inputs = (q, k, v, table,
+    device lengths), cube = a module with build_kernel (for example
+    fgw_amd.operators.mha.current). Returns (combined, info): combined() packs
+    K/V (one launch) and runs the attention, the call the reference times.
+    """
+    name, b, sq, h, d, page, width, lengths, causal = case
+    q, k, v, table, device_lengths = inputs
+    _check_cache(k, v, table, page)
+    lengths = _host_lengths(lengths, b, width * page)
+    offsets, rows, dense = packed_layout(lengths, page, width)
+    cu_rows = torch.tensor(offsets, dtype=torch.int32, device=q.device)
+    dense_table = torch.tensor(dense, dtype=torch.int32, device=q.device)
+    total_pages = offsets[-1] // page
+    attention = cube.build_kernel(b, sq, h, d, rows, width, page, causal, dtype_name,
+                                  device_index, num_splits=splits)
+
+    def gather_pair():
+        dense_k = torch.empty((rows, h, d), dtype=k.dtype, device=k.device)
+        dense_v = torch.empty_like(dense_k)
+        if offsets[-1]:
+            _launch_pack(k, v, table, cu_rows, total_pages, page, dense_k, dense_v)
+        return dense_k, dense_v
+
+    # Exact check of the packed rows against the original pages
+    # (external_cache_gather.py:55-64), outside the timed call.
+    dense_k, dense_v = gather_pair()
+    table_cpu = table.cpu()
+    for original, packed in ((k, dense_k), (v, dense_v)):
+        original_cpu, packed_cpu = original.cpu(), packed.cpu()
+        for i, n in enumerate(lengths):
+            count = -(-n // page)
+            if count:
+                ids = table_cpu[i, :count].long()
+                expected = original_cpu.view(-1, page, h, d)[ids].reshape(-1, h, d)
+                torch.testing.assert_close(packed_cpu[offsets[i]:offsets[i + 1]], expected,
+                                           rtol=0, atol=0, equal_nan=True)
+
+    def combined():
+        dk, dv = gather_pair()
+        return attention(q, dk, dv, dense_table, device_lengths)
+
+    return combined, {
+        "factory": "fgw_mha_pack_pages", "gather_accuracy": "exact_passed",
+        "gather_calls_per_attention": 1 if offsets[-1] else 0,
+        "packed_rows": offsets[-1], "live_rows": sum(lengths), "num_splits": attention.num_splits,
+        "scope": "page-granular pack of K and V in one launch + build_kernel attention",
+        "timed": "K/V allocation, one pack launch, all attention/split/merge kernels; "
+                 "metadata prepared outside timing",
+    }

@@ -164,6 +164,20 @@ int fgw_mha_merge(const fgw_mha_shape* shape, const fgw_mha_plan_t* plan,
 int fgw_mha_gather_kv(const fgw_mha_shape* shape, const fgw_mha_tensors* t, void* out_k,
                       void* out_v, int32_t out_len, hipStream_t stream);
 
+/* Pack the live cache page by page: for request b, pool pages
+ * table[b, 0 .. ceil(len_b / page) - 1] are copied whole, in order, to rows
+ * [cu_rows[b], cu_rows[b + 1]) of out_k / out_v ([cu_rows[B], H, D]); a page
+ * id outside the pool packs as zeros. cu_rows ([B + 1] int32, device) holds
+ * the row offsets (multiples of page_size, cu_rows[0] = 0) and
+ * total_pages = cu_rows[B] / page_size; the caller computes both from
+ * host-known lengths. Replaces the paged-cache gather of the reference's
+ * packed-cache path (benchmarks/mha/external_cache_gather.py:22-49: live
+ * regions rounded up to whole pages, one gather call for K and one for V,
+ * checked row-exactly at :55-64); K and V move in one launch here. */
+int fgw_mha_pack_pages(const fgw_mha_shape* shape, const fgw_mha_tensors* t,
+                       const int32_t* cu_rows, int32_t total_pages, void* out_k, void* out_v,
+                       hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

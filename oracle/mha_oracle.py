@@ -22,6 +22,9 @@ Functions and the reference lines they follow:
   poison_unread        tests/mha/test_mha_paged_accuracy.py:232-238
   bench_inputs         benchmarks/mha/bench_mha_mfu.py:179-188
   gather_packed        benchmarks/mha/external_cache_gather.py:55-64 (row-exact packing)
+  packed_offsets       benchmarks/mha/external_cache_gather.py:28-35 (page-rounded offsets,
+                       identity page table)
+  pack_pages           benchmarks/mha/external_cache_gather.py:55-64 (whole-page copy)
   page_div             Granlund-Montgomery division used by the kernels' page lookup
 
 Pinning (tests/test_oracle.py): the report vectors the reference recorded
@@ -30,7 +33,10 @@ float64 brute-force softmax attention and closed forms (single key, equal
 keys, empty rows) pin reference/chunked_reference; the reference's raw
 partition-merge vectors (tests/mha/test_raw_partial_state.py) and a dense
 comparison pin merge_partials/partial_states; the published FLOP/byte counts
-pin useful_flops/algorithmic_bytes; exhaustive integer checks pin page_div.
+pin useful_flops/algorithmic_bytes; exhaustive integer checks pin page_div;
+row-by-row resolution through physical_rows (live rows) and the original
+pages (page tails), plus closed forms of the offsets, pin packed_offsets and
+pack_pages.
 """
 from __future__ import annotations
 
@@ -234,6 +240,39 @@ def gather_packed(k, v, table, lengths, page_size, out_len):
         ok[bi, :n] = k[rows]
         ov[bi, :n] = v[rows]
     return ok, ov
+
+
+def packed_offsets(lengths: Sequence[int], page_size: int, width: int):
+    """Row offsets of the packed cache and its page table
+    (external_cache_gather.py:28-35): request i's live region rounded up to
+    whole pages, in request order; rows = max(page, total); table row i maps
+    page j to offsets[i] // page + j."""
+    offsets = [0]
+    for n in lengths:
+        offsets.append(offsets[-1] + (int(n) + page_size - 1) // page_size * page_size)
+    rows = max(page_size, offsets[-1])
+    table = torch.tensor([[offsets[i] // page_size + j for j in range(width)]
+                          for i in range(len(lengths))], dtype=torch.int32)
+    return offsets, rows, table
+
+
+def pack_pages(k, v, table, lengths, page_size):
+    """Packed K/V [rows, H, D]: request i's pages table[i, :ceil(len_i / page)]
+    copied whole (rows past len included) to rows [offsets[i], offsets[i + 1])
+    (the expected rows of external_cache_gather.py:55-64); rows past the total
+    are zero."""
+    lengths = [int(n) for n in lengths]
+    offsets, rows, _ = packed_offsets(lengths, page_size, table.shape[1])
+    h, d = k.shape[1:]
+    ok = torch.zeros((rows, h, d), dtype=k.dtype)
+    ov = torch.zeros_like(ok)
+    for i, n in enumerate(lengths):
+        count = (n + page_size - 1) // page_size
+        if count:
+            ids = table[i, :count].long()
+            ok[offsets[i]:offsets[i + 1]] = k.view(-1, page_size, h, d)[ids].reshape(-1, h, d)
+            ov[offsets[i]:offsets[i + 1]] = v.view(-1, page_size, h, d)[ids].reshape(-1, h, d)
+    return ok, ov, offsets
 
 
 def page_divisor(page: int) -> Tuple[int, int]:

@@ -29,7 +29,7 @@ def declared_functions():
 
 def test_every_declared_symbol_is_exported(lib):
     names = declared_functions()
-    assert len(names) == 8, names
+    assert len(names) == 9, names
     for name in names:
         assert hasattr(lib, name), name
     assert set(names) == set(_lib.SIGNATURES)
@@ -116,6 +116,20 @@ def test_fwd_rejects_null_and_misaligned_buffers(lib):
     p.grid = 0  # a plan that does not match the shape is rejected before any launch
     rc = lib.fgw_mha_fwd(ctypes.byref(s), ctypes.byref(p), ctypes.byref(t), None)
     assert rc == _lib.FGW_MHA_EINVAL and b"plan" in lib.fgw_mha_last_error()
+
+
+def test_pack_rejects_bad_arguments_before_any_launch(lib):
+    s = shape(sq=1, kv=512)
+    t = _lib.Tensors()
+    rc = lib.fgw_mha_pack_pages(ctypes.byref(s), ctypes.byref(t), 16, 1, 32, 48, None)
+    assert rc == _lib.FGW_MHA_EINVAL and b"pack needs" in lib.fgw_mha_last_error()
+    t = _lib.Tensors(None, 32, 48, 64, None, None, None, None)
+    rc = lib.fgw_mha_pack_pages(ctypes.byref(s), ctypes.byref(t), 16, 1, 32, 49, None)
+    assert rc == _lib.FGW_MHA_EINVAL and b"aligned" in lib.fgw_mha_last_error()
+    rc = lib.fgw_mha_pack_pages(ctypes.byref(s), ctypes.byref(t), 16, -1, 32, 48, None)
+    assert rc == _lib.FGW_MHA_EINVAL and b"total_pages" in lib.fgw_mha_last_error()
+    # nothing to pack: no launch, success
+    assert lib.fgw_mha_pack_pages(ctypes.byref(s), ctypes.byref(t), 16, 0, 32, 48, None) == 0
 
 
 def test_public_validation_matches_reference_messages():

@@ -233,6 +233,29 @@ def test_gather_packed_matches_explicit_rows():
                 assert torch.count_nonzero(ok[b, pos]) == 0
 
 
+def test_packed_offsets_closed_form():
+    offsets, rows, table = O.packed_offsets([0, 1, 128, 129, 300], 128, 3)
+    assert offsets == [0, 0, 128, 256, 512, 896] and rows == 896
+    assert table.tolist() == [[0, 1, 2], [0, 1, 2], [1, 2, 3], [2, 3, 4], [4, 5, 6]]
+    offsets, rows, _ = O.packed_offsets([0, 0], 16, 2)
+    assert offsets == [0, 0, 0] and rows == 16  # rows never below one page
+
+
+def test_pack_pages_matches_row_by_row_resolution():
+    q, k, v, table, lengths, page = tiny_problem(4, lengths=(3, 0, 10))
+    ok, ov, offsets = O.pack_pages(k, v, table, lengths, page)
+    assert offsets == [0, 3, 3, 15] and ok.shape == (15,) + tuple(k.shape[1:])  # page 3
+    for b in range(3):
+        n = int(lengths[b])
+        live = O.physical_rows(table, b, n, page)
+        for pos in range(offsets[b + 1] - offsets[b]):
+            # live rows through the attention's own resolution, page tails
+            # through the page id of the last live page
+            row = int(live[pos]) if pos < n else int(table[b, pos // page]) * page + pos % page
+            assert torch.equal(ok[offsets[b] + pos], k[row])
+            assert torch.equal(ov[offsets[b] + pos], v[row])
+
+
 def test_bench_inputs_recipe_properties():
     q, k, v, table, lengths = O.bench_inputs(2, 3, 4, 16, 8, 40, torch.bfloat16)
     assert q.shape == (2, 3, 4, 16) and k.shape == (2 * 5 * 8, 4, 16) == v.shape
