@@ -54,10 +54,11 @@ def parse():
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 1 GiB device copy (counter calibration) and exit")
     ap.add_argument("--suite", default="headline",
-                    choices=("headline", "decode-scan", "grid", "prefill", "scans"),
+                    choices=("headline", "decode-scan", "grid", "prefill", "static", "scans"),
                     help="headline: the one-line bench contract (default). decode-scan: "
                          "BASELINE config 4 split scan; grid: config 2 short-Q grid; "
-                         "prefill: Q4096 and Q32768; scans: the three scan suites")
+                         "prefill: Q4096 and Q32768; static: B1H1 static-plan path against "
+                         "the automatic split path; scans: all four scan suites")
     ap.add_argument("--out", default=None, help="scan suites: JSONL file for the records "
                     "(a markdown summary is written beside it)")
     ap.add_argument("--scan-samples", type=int, default=21)
@@ -292,12 +293,76 @@ def suite_prefill(args, emit):
                   "mfu_percent": 100.0 * flops / (back * 1e-6) / 1e12 / PEAK_BF16_TFLOPS})
 
 
+def graph_us(call, calls=20, reps=5):
+    """GPU time per call: `calls` calls captured in one HIP graph, replayed
+    `reps` times (best replay). Host launch work is not in the figure. The
+    first replay's output must equal the eager output bit for bit."""
+    import torch
+    eager = call()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            call()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = [call() for _ in range(calls)]
+    best = float("inf")
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for r in range(reps):
+        a.record()
+        graph.replay()
+        b.record()
+        b.synchronize()
+        best = min(best, a.elapsed_time(b) * 1e3 / calls)
+        if r == 0 and not torch.equal(outs[-1], eager):
+            raise AssertionError("graph replay output differs from the eager call")
+    return best
+
+
+STATIC_SHAPES = ((128, 512), (512, 2048), (1024, 4096), (3712, 4096), (4096, 2048), (8192, 8192),
+                 (16384, 1024), (64, 32768), (5000, 2048), (2048, 16384))
+
+
+def suite_static(args, emit):
+    """B1H1 D128 BF16 full page-128 KV: the static-plan path (choose_stream_plan,
+    the reference's fused B1H1 entry) against the automatic split path, GPU
+    time per call from graph replays; both checked against the oracle."""
+    import torch
+    from fgw_amd.operators.mha import static_schedule as S
+    from fgw_amd.operators.mha.current import build_kernel
+    from fgw_amd.operators.mha.kernels.mha_static_host_hip import build_fused_kernel
+    from oracle import mha_oracle as O
+    dev = torch.device("cuda", 0)
+    for sq, kv in STATIC_SHAPES:
+        host = O.bench_inputs(1, sq, 1, 128, 128, kv, torch.bfloat16)
+        dinputs = [x.to(dev) for x in host]
+        expected = O.chunked_reference(*host, 128, False, 128)
+        auto = build_kernel(1, sq, 1, 128, host[1].shape[0], kv // 128, 128, False, "bfloat16", 0,
+                            full_kv_cache=True)
+        static = build_fused_kernel(sq, kv, host[1].shape[0], 0)
+        _checked(auto, dinputs, expected, torch.bfloat16, f"static-suite auto q{sq} kv{kv}")
+        _checked(static, dinputs, expected, torch.bfloat16, f"static-suite static q{sq} kv{kv}")
+        t_auto = graph_us(lambda: auto(*dinputs))
+        t_static = graph_us(lambda: static(*dinputs))
+        d = static.plan.describe()
+        emit({"suite": "static", "q_len": sq, "kv_len": kv, "auto_us": t_auto,
+              "auto_splits": auto.num_splits, "auto_layout": auto.layout, "static_us": t_static,
+              "static_strategy": d["strategy"], "static_programs": d["programs"],
+              "static_merged_tiles": d["merge_q_tiles"],
+              "static_estimate_us": S.estimate_cost(static.plan)["total_us"],
+              "speedup": t_auto / t_static})
+
+
 def run_scans(args):
     import torch
     torch.cuda.set_device(0)
     suites = {"decode-scan": [suite_decode_scan], "grid": [suite_grid],
-              "prefill": [suite_prefill],
-              "scans": [suite_prefill, suite_decode_scan, suite_grid]}[args.suite]
+              "prefill": [suite_prefill], "static": [suite_static],
+              "scans": [suite_prefill, suite_decode_scan, suite_grid, suite_static]}[args.suite]
     out = open(args.out, "w") if args.out else None
     records = []
 
@@ -324,6 +389,17 @@ def run_scans(args):
 def scan_markdown(records):
     """Summary tables of the scan records (the figures quoted in the docs)."""
     lines = []
+    st = [r for r in records if r["suite"] == "static"]
+    if st:
+        lines += ["## Static plan vs automatic split (B1H1 D128 BF16, full page-128 KV, "
+                  "GPU us/call from graph replays)", "",
+                  "| Q | KV | auto us (splits) | static us | plan (programs, merged tiles) | "
+                  "model us | speedup |", "|---|---|---|---|---|---|---|"]
+        lines += [f"| {r['q_len']} | {r['kv_len']} | {r['auto_us']:.1f} (s{r['auto_splits']}) | "
+                  f"{r['static_us']:.1f} | {r['static_strategy']} ({r['static_programs']}, "
+                  f"{r['static_merged_tiles']}) | {r['static_estimate_us']:.1f} | "
+                  f"{r['speedup']:.2f} |" for r in st]
+        lines.append("")
     pre = [r for r in records if r["suite"] == "prefill"]
     if pre:
         lines += ["## Prefill (B2 H8 D128 BF16 page 128, KV 2048)", "",

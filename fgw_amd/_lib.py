@@ -48,6 +48,12 @@ class Tensors(ctypes.Structure):
                 ("parts", c_void_p), ("lse", c_void_p)]
 
 
+class Schedule(ctypes.Structure):
+    _fields_ = [("segments", c_void_p), ("seg_offsets", c_void_p), ("merges", c_void_p),
+                ("programs", c_int32), ("n_merges", c_int32), ("slots", c_int32),
+                ("block_keys", c_int32)]
+
+
 # name -> (argtypes); every function returns int.
 SIGNATURES = {
     "fgw_mha_abi_version": (),
@@ -64,6 +70,10 @@ SIGNATURES = {
                           c_int32, c_void_p),
     "fgw_mha_pack_pages": (ctypes.POINTER(Shape), ctypes.POINTER(Tensors), c_void_p, c_int32,
                            c_void_p, c_void_p, c_void_p),
+    "fgw_mha_static_local": (ctypes.POINTER(Shape), ctypes.POINTER(Tensors),
+                             ctypes.POINTER(Schedule), c_void_p),
+    "fgw_mha_static_merge": (ctypes.POINTER(Shape), ctypes.POINTER(Tensors),
+                             ctypes.POINTER(Schedule), c_void_p),
 }
 
 _lock = threading.Lock()

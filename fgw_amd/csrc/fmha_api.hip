@@ -61,6 +61,15 @@ hipError_t launch_gather(const GatherParams& p, hipStream_t stream) {
   return hipGetLastError();
 }
 
+hipError_t launch_group_merge(bool bf16, const GroupMergeParams& p, int groups,
+                              hipStream_t stream) {
+  if (bf16)
+    group_merge_kernel<true><<<dim3((unsigned)groups), dim3(kMergeThreads), 0, stream>>>(p);
+  else
+    group_merge_kernel<false><<<dim3((unsigned)groups), dim3(kMergeThreads), 0, stream>>>(p);
+  return hipGetLastError();
+}
+
 hipError_t launch_pack(const PackParams& p, int total_pages, hipStream_t stream) {
   const int64_t wgs = (int64_t)total_pages * p.wg_per_page;
   pack_pages_kernel<<<dim3((unsigned)wgs), dim3(kPackThreads), 0, stream>>>(p);
@@ -203,7 +212,30 @@ FwdParams make_params(const fgw_mha_shape* s, const fgw_mha_plan_t* p, const fgw
   f.mode = mode;
   page_divisor((uint32_t)s->page_size, &f.page_magic, &f.page_shift);
   f.scale_log2 = (float)(1.4426950408889634 / __builtin_sqrt((double)s->dim));
+  f.segs = nullptr;
+  f.seg_offsets = nullptr;
+  f.slots = 0;
+  f.seg_scale = 1;
   return f;
+}
+
+// Checks shared by the static-schedule entries.
+int check_schedule(const fgw_mha_shape* s, const fgw_mha_schedule* sc) {
+  int rc = check_shape(s);
+  if (rc) return rc;
+  if (!sc) return fail(FGW_MHA_EINVAL, "schedule is NULL");
+  const int bn = Cfg<true, 128, kLayoutQuery>::BN;
+  if (sc->block_keys <= 0 || sc->block_keys % bn)
+    return fail(FGW_MHA_EINVAL, "schedule block_keys must be a positive multiple of %d", bn);
+  if (sc->programs < 1 || !sc->seg_offsets || !sc->segments)
+    return fail(FGW_MHA_EINVAL, "schedule needs programs >= 1, segments and seg_offsets");
+  if (sc->slots < 0 || sc->n_merges < 0 || (sc->n_merges > 0 && !sc->merges))
+    return fail(FGW_MHA_EINVAL, "schedule slots and merges must be consistent");
+  const int rows = rows_per_tile(kLayoutQuery);
+  const int64_t tasks = (int64_t)s->batch * s->heads * ((s->sq + rows - 1) / rows);
+  if (tasks > INT32_MAX || (int64_t)sc->slots * rows > INT32_MAX)
+    return fail(FGW_MHA_EUNSUPPORTED, "schedule exceeds 2^31 tasks or partial rows");
+  return FGW_MHA_OK;
 }
 
 int launch_partial_kernel(const fgw_mha_shape* s, const fgw_mha_plan_t* p,
@@ -387,6 +419,60 @@ int fgw_mha_gather_kv(const fgw_mha_shape* s, const fgw_mha_tensors* t, void* ou
   page_divisor((uint32_t)s->page_size, &g.page_magic, &g.page_shift);
   const hipError_t err = launch_gather(g, stream);
   return err == hipSuccess ? FGW_MHA_OK : hip_fail(err, "gather kernel launch");
+}
+
+int fgw_mha_static_local(const fgw_mha_shape* s, const fgw_mha_tensors* t,
+                         const fgw_mha_schedule* sc, hipStream_t stream) {
+  int rc = check_schedule(s, sc);
+  if (!rc) rc = check_tensors(t, true, true, sc->slots > 0);
+  if (rc) return rc;
+  const int dpad = dim_tile(s->dim);
+  const FwdEntry e = fwd_entry(s->dtype == FGW_MHA_BFLOAT16, dpad, kLayoutQuery);
+  if (!e.launch) return fail(FGW_MHA_EUNSUPPORTED, "no kernel for dim tile %d", dpad);
+  fgw_mha_plan_t p;
+  std::memset(&p, 0, sizeof(p));
+  p.layout = kLayoutQuery;
+  p.rows_per_tile = rows_per_tile(kLayoutQuery);
+  p.q_tiles = (s->sq + p.rows_per_tile - 1) / p.rows_per_tile;
+  p.num_splits = 1;
+  p.work_items = 0;
+  p.dim_padded = dpad;
+  FwdParams f = make_params(s, &p, t, 2);
+  f.segs = sc->segments;
+  f.seg_offsets = sc->seg_offsets;
+  f.slots = sc->slots;
+  f.seg_scale = sc->block_keys / Cfg<true, 128, kLayoutQuery>::BN;
+  const hipError_t err = e.launch(f, sc->programs, stream);
+  return err == hipSuccess ? FGW_MHA_OK : hip_fail(err, "static schedule kernel launch");
+}
+
+int fgw_mha_static_merge(const fgw_mha_shape* s, const fgw_mha_tensors* t,
+                         const fgw_mha_schedule* sc, hipStream_t stream) {
+  int rc = check_schedule(s, sc);
+  if (rc) return rc;
+  if (sc->n_merges == 0) return FGW_MHA_OK;
+  if (!t || !t->out || !aligned16(t->out) || !t->parts || !t->lse || !aligned16(t->parts))
+    return fail(FGW_MHA_EINVAL, "merge needs out, parts and lse; out and parts 16-byte aligned");
+  GroupMergeParams g;
+  g.parts = t->parts;
+  g.lse = t->lse;
+  g.groups = sc->merges;
+  g.out = t->out;
+  g.sq = s->sq;
+  g.heads = s->heads;
+  g.dim = s->dim;
+  g.rows_tile = rows_per_tile(kLayoutQuery);
+  g.q_tiles = (s->sq + g.rows_tile - 1) / g.rows_tile;
+  g.slots = sc->slots;
+  g.tasks = s->batch * s->heads * g.q_tiles;
+  // One (row, 4 dims) per thread: kMergeThreads / (D / 4) rows per workgroup.
+  g.rows_wg = kMergeThreads / (s->dim / 4) > 0 ? kMergeThreads / (s->dim / 4) : 1;
+  g.wg_per_group = (g.rows_tile + g.rows_wg - 1) / g.rows_wg;
+  if ((int64_t)sc->n_merges * g.wg_per_group > INT32_MAX)
+    return fail(FGW_MHA_EUNSUPPORTED, "merge groups exceed the grid");
+  const hipError_t err = launch_group_merge(s->dtype == FGW_MHA_BFLOAT16, g,
+                                            sc->n_merges * g.wg_per_group, stream);
+  return err == hipSuccess ? FGW_MHA_OK : hip_fail(err, "group merge kernel launch");
 }
 
 int fgw_mha_pack_pages(const fgw_mha_shape* s, const fgw_mha_tensors* t, const int32_t* cu_rows,

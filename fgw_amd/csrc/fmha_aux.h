@@ -15,52 +15,59 @@ namespace fgw_mha {
 // once per chunk. Empty splits (LSE -1e30) carry zero weight and an
 // all-empty row is exactly zero.
 constexpr int kMergeChunk = 16;
+// One (row, 4 dims): split s's LSE at ls[s * lse_stride], its part at
+// ps[s * part_stride]; the result goes to dst in the input dtype.
+template <bool BF16>
+__device__ __forceinline__ void merge_one(const float* ls, int64_t lse_stride, const float* ps,
+                                          int64_t part_stride, int splits, u16* dst) {
+  using E = Elem<BF16>;
+  float peak = kNegBig, tot = 0.0f;
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int s0 = 0; s0 < splits; s0 += kMergeChunk) {
+    float x[kMergeChunk];
+    f32x4 v[kMergeChunk];
+#pragma unroll
+    for (int i = 0; i < kMergeChunk; ++i) {
+      const int s = s0 + i < splits ? s0 + i : splits - 1;  // clamped; weight 0 below
+      x[i] = ls[(int64_t)s * lse_stride];
+      v[i] = *reinterpret_cast<const f32x4*>(ps + (int64_t)s * part_stride);
+    }
+    float cpeak = peak;
+#pragma unroll
+    for (int i = 0; i < kMergeChunk; ++i) {
+      const bool live = s0 + i < splits && x[i] > -1.0e29f;
+      cpeak = live ? fmaxf(cpeak, x[i]) : cpeak;
+    }
+    const float keep = expf(peak - cpeak);  // 0 while nothing was live, 1 if unchanged
+    tot *= keep;
+    acc *= keep;
+#pragma unroll
+    for (int i = 0; i < kMergeChunk; ++i) {
+      const bool live = s0 + i < splits && x[i] > -1.0e29f;
+      const float wgt = live ? expf(x[i] - cpeak) : 0.0f;
+      tot += wgt;
+      acc += live ? v[i] * wgt : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    peak = cpeak;
+  }
+  const float inv = 1.0f / fmaxf(tot, 1.0e-30f);
+  u32x2 w;
+  w.x = E::pack2(acc[0] * inv, acc[1] * inv);
+  w.y = E::pack2(acc[2] * inv, acc[3] * inv);
+  *reinterpret_cast<u32x2*>(dst) = w;
+}
+
 template <bool BF16>
 __device__ __forceinline__ void merge_rows(const float* parts, const float* lse, void* out, int sq,
                                            int heads, int dim, int splits, int b, int h, int q0,
                                            int rows, int tid, int nthreads) {
-  using E = Elem<BF16>;
   const int d4n = dim / 4;
   const int64_t bhs = ((int64_t)b * heads + h) * splits;
   for (int idx = tid; idx < rows * d4n; idx += nthreads) {
     const int q = q0 + idx / d4n, d0 = 4 * (idx % d4n);
-    const float* ls = lse + bhs * sq + q;
-    const float* ps = parts + (bhs * sq + q) * dim + d0;
-    float peak = kNegBig, tot = 0.0f;
-    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int s0 = 0; s0 < splits; s0 += kMergeChunk) {
-      float x[kMergeChunk];
-      f32x4 v[kMergeChunk];
-#pragma unroll
-      for (int i = 0; i < kMergeChunk; ++i) {
-        const int s = s0 + i < splits ? s0 + i : splits - 1;  // clamped; weight 0 below
-        x[i] = ls[(int64_t)s * sq];
-        v[i] = *reinterpret_cast<const f32x4*>(ps + (int64_t)s * sq * dim);
-      }
-      float cpeak = peak;
-#pragma unroll
-      for (int i = 0; i < kMergeChunk; ++i) {
-        const bool live = s0 + i < splits && x[i] > -1.0e29f;
-        cpeak = live ? fmaxf(cpeak, x[i]) : cpeak;
-      }
-      const float keep = expf(peak - cpeak);  // 0 while nothing was live, 1 if unchanged
-      tot *= keep;
-      acc *= keep;
-#pragma unroll
-      for (int i = 0; i < kMergeChunk; ++i) {
-        const bool live = s0 + i < splits && x[i] > -1.0e29f;
-        const float wgt = live ? expf(x[i] - cpeak) : 0.0f;
-        tot += wgt;
-        acc += live ? v[i] * wgt : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      }
-      peak = cpeak;
-    }
-    const float inv = 1.0f / fmaxf(tot, 1.0e-30f);
-    u32x2 w;
-    w.x = E::pack2(acc[0] * inv, acc[1] * inv);
-    w.y = E::pack2(acc[2] * inv, acc[3] * inv);
     u16* dst = static_cast<u16*>(out) + (((int64_t)b * sq + q) * heads + h) * dim + d0;
-    *reinterpret_cast<u32x2*>(dst) = w;
+    merge_one<BF16>(lse + bhs * sq + q, sq, parts + (bhs * sq + q) * dim + d0,
+                    (int64_t)sq * dim, splits, dst);
   }
 }
 
@@ -75,6 +82,32 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(MergeParams p, int
   const int rows = p.sq - q0 < rows_per_wg ? p.sq - q0 : rows_per_wg;
   merge_rows<BF16>(p.parts, p.lse, p.out, p.sq, p.heads, p.dim, p.splits, bh / p.heads,
                    bh % p.heads, q0, rows, threadIdx.x, kMergeThreads);
+}
+
+// Merge of the static schedule's split tiles: group g (task, first slot,
+// slots) is merged by groups_wg workgroups, workgroup j taking rows
+// [j rows_wg, (j + 1) rows_wg) of the tile; the partials of slot s are in
+// parts [s, rows_tile, D]. Groups a host plan cannot produce are skipped.
+template <bool BF16>
+__global__ __launch_bounds__(kMergeThreads) void group_merge_kernel(GroupMergeParams p) {
+  const int32_t* gr = p.groups + 3 * (int64_t)(blockIdx.x / (unsigned)p.wg_per_group);
+  const int task = gr[0], first = gr[1], count = gr[2];
+  if (task < 0 || task >= p.tasks || first < 0 || count < 1 || first + count > p.slots) return;
+  const int qt = task % p.q_tiles;
+  const int bh = task / p.q_tiles;
+  const int h = bh % p.heads, b = bh / p.heads;
+  const int q0 = qt * p.rows_tile;
+  const int tile_rows = p.sq - q0 < p.rows_tile ? p.sq - q0 : p.rows_tile;
+  const int r0 = (int)(blockIdx.x % (unsigned)p.wg_per_group) * p.rows_wg;
+  const int rows = tile_rows - r0 < p.rows_wg ? tile_rows - r0 : p.rows_wg;
+  const int d4n = p.dim / 4;
+  const int64_t slot_rows = (int64_t)p.rows_tile;
+  for (int idx = threadIdx.x; idx < rows * d4n; idx += kMergeThreads) {
+    const int r = r0 + idx / d4n, d0 = 4 * (idx % d4n);
+    u16* dst = static_cast<u16*>(p.out) + (((int64_t)b * p.sq + q0 + r) * p.heads + h) * p.dim + d0;
+    merge_one<BF16>(p.lse + first * slot_rows + r, slot_rows,
+                    p.parts + (first * slot_rows + r) * p.dim + d0, slot_rows * p.dim, count, dst);
+  }
 }
 
 // Packed copy of the live cache: out[b, pos] = cache[phys_row(b, pos)] for

@@ -10,6 +10,10 @@
 //   s = q.k * D^-0.5, running max m, p = exp(s - m) rounded to the input dtype
 //   for the PV product, l = l*alpha + sum(p) in fp32, O = alpha*O + P.V,
 //   output O / max(l, 1e-30); partial mode stores O/l and LSE = ln(l) + m.
+// Static-schedule mode (query layout only) takes the work items from a host
+// plan instead: each program runs its segments (task, key-block range, slot)
+// and writes whole tiles to the output, cut tiles to their partial slot
+// (operators/mha/static_schedule.py:8-16).
 // The exponentials run as exp2 on log2(e)-prescaled scores, against an
 // exponent reference m that moves only when a block's row sums leave a bound
 // (online_softmax): mathematically the same O/l and LSE. The head dim is
@@ -523,11 +527,18 @@ __device__ __forceinline__ void pv_block(const unsigned char* vt, const Lanes<C>
   }
 }
 
+// Output of one (row, 4 dims): the normalised output in mode 0 and for a
+// static-schedule segment without a slot; O/l in the partial layout of mode 1
+// or in the slot rows of mode 2 otherwise.
 template <class C>
 __device__ __forceinline__ void store_row(const FwdParams& p, int b, int h, int split, int qrow,
-                                          int d0, f32x4 val, float inv) {
+                                          int d0, f32x4 val, float inv, int slot = -1,
+                                          int q0 = 0) {
   using E = Elem<C::BF16>;
-  if (p.mode == 0) {
+  if (p.mode == 2 && slot >= 0) {
+    float* dst = p.parts + ((int64_t)slot * C::ROWS_TILE + (qrow - q0)) * p.dim + d0;
+    *reinterpret_cast<f32x4*>(dst) = val * inv;
+  } else if (p.mode != 1) {
     u16* dst = static_cast<u16*>(p.out) + (((int64_t)b * p.sq + qrow) * p.heads + h) * p.dim + d0;
     u32x2 w;
     w.x = E::pack2(val[0] * inv, val[1] * inv);
@@ -570,15 +581,32 @@ __global__ __launch_bounds__(C::THREADS) void fwd_kernel(FwdParams p,
 
   const int grid = gridDim.x;
   const int prog = xcd_remap(blockIdx.x, grid);
-  const int per = p.work / grid, rem = p.work % grid;
-  const int first = prog * per + (prog < rem ? prog : rem);
-  const int count = per + (prog < rem ? 1 : 0);
+  int first, count;
+  if (p.mode == 2) {  // static schedule: this program's segments
+    first = p.seg_offsets[prog];
+    count = p.seg_offsets[prog + 1] - first;
+  } else {  // contiguous range of work items
+    const int per = p.work / grid, rem = p.work % grid;
+    first = prog * per + (prog < rem ? prog : rem);
+    count = per + (prog < rem ? 1 : 0);
+  }
   const int capacity = p.width * p.page_size;
+  const int tasks = p.batch * p.heads * p.q_tiles;
 
   for (int it = 0; it < count; ++it) {
-    int w = first + it;
-    const int split = w % p.splits;
-    w /= p.splits;
+    int w = first + it, split = 0, slot = -1, seg_lo = 0, seg_hi = 0;
+    if (p.mode == 2) {
+      const int32_t* sg = p.segs + 4 * (int64_t)w;
+      w = sg[0];
+      seg_lo = sg[1] * p.seg_scale;
+      seg_hi = (sg[1] + sg[2]) * p.seg_scale;
+      slot = sg[3];
+      // Segments a host plan cannot produce are skipped whole (uniform).
+      if (w < 0 || w >= tasks || slot >= p.slots || sg[1] < 0 || sg[2] < 0) continue;
+    } else {
+      split = w % p.splits;
+      w /= p.splits;
+    }
     const int qt = w % p.q_tiles;
     w /= p.q_tiles;
     const int h = w % p.heads;
@@ -594,8 +622,14 @@ __global__ __launch_bounds__(C::THREADS) void fwd_kernel(FwdParams p,
     int max_vis = p.causal ? len - p.sq + tile_last + 1 : len;
     max_vis = max_vis < 0 ? 0 : (max_vis > len ? len : max_vis);
     const int nblk = (max_vis + C::BN - 1) / C::BN;
-    const int blk_begin = (int)((int64_t)nblk * split / p.splits);
-    const int blk_end = (int)((int64_t)nblk * (split + 1) / p.splits);
+    int blk_begin, blk_end;
+    if (p.mode == 2) {  // the segment's blocks that hold visible keys
+      blk_end = seg_hi < nblk ? seg_hi : nblk;
+      blk_begin = seg_lo < blk_end ? seg_lo : blk_end;
+    } else {
+      blk_begin = (int)((int64_t)nblk * split / p.splits);
+      blk_end = (int)((int64_t)nblk * (split + 1) / p.splits);
+    }
     const int cnt = blk_end - blk_begin;
     const int my_n = cnt > wk ? (cnt - wk + C::NWK - 1) / C::NWK : 0;
 
@@ -682,11 +716,13 @@ __global__ __launch_bounds__(C::THREADS) void fwd_kernel(FwdParams p,
             const int d0 = 32 * dt + 8 * gq + 4 * hh;
             if (d0 < p.dim) {
               f32x4 val = {o[dt][4 * gq], o[dt][4 * gq + 1], o[dt][4 * gq + 2], o[dt][4 * gq + 3]};
-              store_row<C>(p, b, h, split, qrow, d0, val, inv);
+              store_row<C>(p, b, h, split, qrow, d0, val, inv, slot, q0);
             }
           }
-        if (p.mode != 0 && hh == 0) {
+        if (p.mode == 1 && hh == 0) {
           p.lse[(((int64_t)b * p.heads + h) * p.splits + split) * p.sq + qrow] = lse_of(m, tot);
+        } else if (p.mode == 2 && slot >= 0 && hh == 0) {
+          p.lse[(int64_t)slot * C::ROWS_TILE + (qrow - q0)] = lse_of(m, tot);
         }
       }
     } else {
@@ -727,7 +763,7 @@ __global__ __launch_bounds__(C::THREADS) void fwd_kernel(FwdParams p,
                    wt;
           }
           store_row<C>(p, b, h, split, row, d0, acc, 1.0f / fmaxf(t2, 1.0e-30f));
-          if (p.mode != 0 && d0 == 0) {
+          if (p.mode == 1 && d0 == 0) {
             p.lse[(((int64_t)b * p.heads + h) * p.splits + split) * p.sq + row] = lse_of(mm, t2);
           }
         }

@@ -27,10 +27,20 @@ struct FwdParams {
   int32_t splits;
   int32_t q_tiles;        // ceil(Sq / rows per tile)
   int32_t work;           // B * H * q_tiles * splits
-  int32_t mode;           // 0: normalised output, 1: partial (O/l, LSE)
+  int32_t mode;           // 0: normalised output, 1: partial (O/l, LSE), 2: static schedule
   uint32_t page_magic;    // division of positions by page_size
   uint32_t page_shift;
   float scale_log2;       // dim^-0.5 * log2(e)
+  // Static schedule (mode 2, query layout): program p runs segments
+  // [seg_offsets[p], seg_offsets[p + 1]) of segs, each (task, first key
+  // block, key blocks, slot) with task = (b H + h) q_tiles + q tile and key
+  // blocks of the kernel's BN keys. slot < 0 writes the normalised output;
+  // slot >= 0 writes O/l to parts [slot, rows per tile, D] and the LSE to
+  // lse [slot, rows per tile].
+  const int32_t* segs;
+  const int32_t* seg_offsets;
+  int32_t slots;
+  int32_t seg_scale;  // kernel key blocks per schedule key block
 };
 
 struct MergeParams {
@@ -38,6 +48,17 @@ struct MergeParams {
   const float* lse;       // [B, H, S, Sq]
   void* out;              // [B, Sq, H, D]
   int32_t batch, sq, heads, dim, splits;
+};
+
+// Merge of the static schedule's split tiles: group g = (task, first slot,
+// slots) merges parts [first .. first + slots) of one query tile.
+struct GroupMergeParams {
+  const float* parts;     // [slots, rows per tile, D]
+  const float* lse;       // [slots, rows per tile]
+  const int32_t* groups;  // [G, 3]
+  void* out;              // [B, Sq, H, D]
+  int32_t sq, heads, dim, q_tiles, rows_tile, slots, tasks;
+  int32_t rows_wg, wg_per_group;  // rows per workgroup, workgroups per group
 };
 
 struct GatherParams {

@@ -406,7 +406,7 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p,
             store_row<C>(p, b, h, split, qrow, d0, val, inv);
           }
         }
-      if (p.mode != 0 && hh == 0) {
+      if (p.mode == 1 && hh == 0) {
         p.lse[(((int64_t)b * p.heads + h) * p.splits + split) * p.sq + qrow] = lse_of(m, tot);
       }
     }

@@ -26,6 +26,7 @@ FwdEntry fwd_entry(bool bf16, int dpad, int layout);
 hipError_t launch_merge(bool bf16, const MergeParams& p, hipStream_t stream);
 hipError_t launch_gather(const GatherParams& p, hipStream_t stream);
 hipError_t launch_pack(const PackParams& p, int total_pages, hipStream_t stream);
+hipError_t launch_group_merge(bool bf16, const GroupMergeParams& p, int groups, hipStream_t stream);
 
 }  // namespace fgw_mha
 

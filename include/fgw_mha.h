@@ -164,6 +164,40 @@ int fgw_mha_merge(const fgw_mha_shape* shape, const fgw_mha_plan_t* plan,
 int fgw_mha_gather_kv(const fgw_mha_shape* shape, const fgw_mha_tensors* t, void* out_k,
                       void* out_v, int32_t out_len, hipStream_t stream);
 
+/* Static KV-block schedule over the query layout's 128-row tiles: a host
+ * plan assigns every (task, key block) unit to one program as contiguous
+ * segments; tiles cut across programs get a partial slot each and are merged
+ * afterwards. task = (b H + h) ceil(Sq / 128) + q tile. Mirrors the plan the
+ * reference's static host path consumes (operators/mha/static_schedule.py:
+ * 8-16: segments (Q tile, first KV block, KV blocks, slot), merges (Q tile,
+ * first slot, slots), slot -1 = written directly). */
+typedef struct fgw_mha_schedule {
+  const int32_t* segments;    /* device [n_segments, 4]: task, first block, blocks, slot (-1: direct) */
+  const int32_t* seg_offsets; /* device [programs + 1]: segments of program p */
+  const int32_t* merges;      /* device [n_merges, 3]: task, first slot, slots */
+  int32_t programs;           /* grid of the local kernel */
+  int32_t n_merges;
+  int32_t slots;              /* partial slots: parts [slots, 128, D], lse [slots, 128] fp32 */
+  int32_t block_keys;         /* keys per schedule block, a multiple of 64 (the reference: 128) */
+} fgw_mha_schedule;
+
+/* Local phase of a static schedule: every program runs its segments; direct
+ * segments write the normalised output rows of their tile, the others O/l
+ * and LSE into their slot. Segments and merges a valid plan cannot contain
+ * (task or slot out of range, negative blocks) are skipped; key blocks past
+ * a request's length are clamped. Replaces the static host candidate's
+ * local kernel (operators/mha/kernels/mha_static_host_candidate.py:457-460,
+ * :511-519). */
+int fgw_mha_static_local(const fgw_mha_shape* shape, const fgw_mha_tensors* t,
+                         const fgw_mha_schedule* schedule, hipStream_t stream);
+
+/* Merge phase: one workgroup per merge group combines its slots into the
+ * output rows of its tile (the LSE merge of fgw_mha_merge). Replaces the
+ * static host candidate's merge kernel (mha_static_host_candidate.py:
+ * 476-480, :521-525). No launch when n_merges is 0. */
+int fgw_mha_static_merge(const fgw_mha_shape* shape, const fgw_mha_tensors* t,
+                         const fgw_mha_schedule* schedule, hipStream_t stream);
+
 /* Pack the live cache page by page: for request b, pool pages
  * table[b, 0 .. ceil(len_b / page) - 1] are copied whole, in order, to rows
  * [cu_rows[b], cu_rows[b + 1]) of out_k / out_v ([cu_rows[B], H, D]); a page
