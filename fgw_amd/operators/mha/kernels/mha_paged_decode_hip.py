@@ -226,8 +226,9 @@ def build_kernel(batch, sq, heads, dim, pool_rows, width, page_size, causal, dty
     cube_general.py:17, :45) and layout ("query" = 4 waves split 128 query
     rows; "prefill" = 8 waves split 256 query rows in two groups that
     alternate matrix and softmax phases, D in (32, 128]; "key" = waves split
-    key blocks; None: key for Sq <= 32, prefill when its 256-row tiles fill
-    the device, else query).
+    key blocks; None: key for Sq <= 32; prefill when its 256-row tiles fill
+    the device, or, with KV splits, for non-causal D 128 from Sq 1024; else
+    query).
     """
     requested_split_policy = split_policy
     if split_policy not in SPLIT_POLICIES:
