@@ -112,18 +112,17 @@ bool has_prefill(int dpad) { return dpad == 64 || dpad == 128; }
 //  - when its 256-row query tiles alone give every resident program of the
 //    device a work item (measured faster than the query layout: B2 H8 D128
 //    BF16, KV 2048, Q 4096 and Q 32768);
-//  - for fewer tiles, where KV splits fill the device, at head-dim tile 128,
-//    non-causal, from Q 1024 on: measured with the automatic splits of both
-//    layouts (B2 H8, B1 H8, B1 H16, B4 H8; KV 2048-8192) the prefill layout
-//    is 1.06-1.19x faster there (on par at Q 512).
-// Shorter, causal or other head-dim cases keep the query layout.
+//  - for fewer tiles, where KV splits fill the device, from Q 1024 on:
+//    measured with the automatic splits of both layouts (B1-B4, H8-H16,
+//    KV 2048-8192, head-dim tiles 64 and 128, causal or not) the prefill
+//    layout is 1.06-1.25x faster there (on par at Q 512).
+// Shorter cases keep the query layout.
 bool auto_prefill(const fgw_mha_shape* s, const fgw_mha_device_info* dev, int dpad) {
   if (!has_prefill(dpad) || s->sq < 256) return false;
   const int rows = 256;
   const int64_t tiles = (int64_t)s->batch * s->heads * ((s->sq + rows - 1) / rows);
   const int wg = dev->wg_per_cu[kLayoutPrefill] > 0 ? dev->wg_per_cu[kLayoutPrefill] : 1;
-  if (tiles >= (int64_t)dev->num_cus * wg) return true;
-  return dpad == 128 && !s->causal && s->sq >= 1024;
+  return tiles >= (int64_t)dev->num_cus * wg || s->sq >= 1024;
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }

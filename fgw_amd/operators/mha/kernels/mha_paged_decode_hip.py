@@ -227,7 +227,7 @@ def build_kernel(batch, sq, heads, dim, pool_rows, width, page_size, causal, dty
     rows; "prefill" = 8 waves split 256 query rows in two groups that
     alternate matrix and softmax phases, D in (32, 128]; "key" = waves split
     key blocks; None: key for Sq <= 32; prefill when its 256-row tiles fill
-    the device, or, with KV splits, for non-causal D 128 from Sq 1024; else
+    the device, or, with KV splits, from Sq 1024, for D in (32, 128]; else
     query).
     """
     requested_split_policy = split_policy

@@ -49,13 +49,13 @@ def test_plan_headline_shapes(lib):
     assert prefill.threads == 512
     mid = _lib.plan(shape(sq=128, kv=2048), _lib.Request(0, -1, -1), DEVICE)
     assert (mid.layout, mid.rows_per_tile, mid.threads) == (0, 128, 256)  # short Q: query layout
-    # 64 prefill tiles, KV splits fill the device: prefill layout from Q 1024 (D 128,
-    # non-causal); Q 512 and causal keep the query layout.
+    # 64 prefill tiles, KV splits fill the device: prefill layout from Q 1024 (head-dim
+    # tiles 64 and 128, causal or not); Q 512 keeps the query layout.
     few = _lib.plan(shape(sq=1024, kv=2048), _lib.Request(0, -1, -1), DEVICE)
     assert (few.layout, few.q_tiles, few.num_splits, few.work_items) == (2, 4, 4, 256)
     assert _lib.plan(shape(sq=512, kv=2048), _lib.Request(0, -1, -1), DEVICE).layout == 0
-    assert _lib.plan(shape(sq=1024, kv=2048, causal=1), _lib.Request(0, -1, -1), DEVICE).layout == 0
-    assert _lib.plan(shape(sq=1024, kv=2048, d=64), _lib.Request(0, -1, -1), DEVICE).layout == 0
+    assert _lib.plan(shape(sq=1024, kv=2048, causal=1), _lib.Request(0, -1, -1), DEVICE).layout == 2
+    assert _lib.plan(shape(sq=1024, kv=2048, d=64), _lib.Request(0, -1, -1), DEVICE).layout == 2
     wide = _lib.plan(shape(sq=4096, kv=2048, d=256), _lib.Request(0, -1, -1), DEVICE)
     assert (wide.layout, wide.dim_padded) == (0, 256)  # no prefill kernel for D > 128
     narrow = _lib.plan(shape(sq=4096, kv=2048, d=32), _lib.Request(0, -1, -1), DEVICE)
