@@ -341,7 +341,12 @@ int fgw_mha_plan(const fgw_mha_shape* s, const fgw_mha_request* req,
   int64_t grid = work;
   if (req->persistent_programs < -1)
     return fail(FGW_MHA_EINVAL, "persistent_programs must be -1, 0 or positive");
-  if (req->persistent_programs == -1) {
+  if (req->persistent_programs == -1 && !s->causal) {
+    // Device cap: the resident workgroups of all CUs loop over contiguous
+    // ranges of work items. Causal work items differ in size (and with
+    // Sq > len many are empty), so causal plans keep one workgroup per work
+    // item and let the hardware dispatcher balance them: measured 1.06-2.5x
+    // faster than the cap for causal prefill with more tiles than programs.
     const int wg = dev->wg_per_cu[layout] > 0 ? dev->wg_per_cu[layout] : 1;
     const int64_t cap = (int64_t)dev->num_cus * wg;
     grid = work < cap ? work : cap;

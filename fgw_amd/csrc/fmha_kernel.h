@@ -607,7 +607,9 @@ __global__ __launch_bounds__(C::THREADS) void fwd_kernel(FwdParams p,
       split = w % p.splits;
       w /= p.splits;
     }
-    const int qt = w % p.q_tiles;
+    // Causal tiles outside a static schedule: the last (heaviest) first, so
+    // that a dispatcher or a persistent program starts the long items early.
+    const int qt = p.causal && p.mode != 2 ? p.q_tiles - 1 - w % p.q_tiles : w % p.q_tiles;
     w /= p.q_tiles;
     const int h = w % p.heads;
     const int b = w / p.heads;

@@ -245,7 +245,9 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p,
     int w = first + it;
     const int split = w % p.splits;
     w /= p.splits;
-    const int qt = w % p.q_tiles;
+    // Causal tiles: the last (heaviest) first, so that a dispatcher or a
+    // persistent program starts the long work items early.
+    const int qt = p.causal ? p.q_tiles - 1 - w % p.q_tiles : w % p.q_tiles;
     w /= p.q_tiles;
     const int h = w % p.heads;
     const int b = w / p.heads;

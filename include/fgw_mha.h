@@ -77,7 +77,7 @@ typedef struct {
  * (v7.py:43-46, :94-113; v7_experimental.py:29-30 persistent_programs). */
 typedef struct {
   int32_t num_splits;          /* 0 = automatic; else 1,2,4,...,128 */
-  int32_t persistent_programs; /* -1 = CU-derived cap, 0 = uncapped grid, n > 0 = cap */
+  int32_t persistent_programs; /* -1 = CU-derived cap (uncapped for causal), 0 = uncapped grid, n > 0 = cap */
   int32_t layout;              /* fgw_mha_layout */
 } fgw_mha_request;
 

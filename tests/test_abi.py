@@ -70,6 +70,11 @@ def test_plan_headline_shapes(lib):
     assert uncapped.grid == uncapped.work_items
     capped = _lib.plan(shape(sq=32768, kv=2048), _lib.Request(0, 28, -1), DEVICE)
     assert capped.grid == 28
+    # causal work items differ in size: the device request leaves one workgroup per item
+    causal = _lib.plan(shape(sq=32768, kv=2048, causal=1), _lib.Request(0, -1, -1), DEVICE)
+    assert causal.grid == causal.work_items == 2 * 8 * 128
+    causal_capped = _lib.plan(shape(sq=32768, kv=2048, causal=1), _lib.Request(0, 28, -1), DEVICE)
+    assert causal_capped.grid == 28
 
 
 def test_plan_split_rules(lib):
