@@ -1,11 +1,11 @@
 """Benchmark of the paged MHA operator on one MI355X.
 
-Headline workload: Q4096 / KV2048, B2 H8 D128 BF16,
+Headline workload (benchmark config 3): Q4096 / KV2048, B2 H8 D128 BF16,
 page 128, non-causal, full cache, shuffled block table, inputs resident in
 HBM. One step = one call of the launch callable (output allocation and every
 kernel included, compile and H2D excluded), as the reference times it
 (benchmarks/mha/bench_mha_mfu.py:221-247). Alongside: Q1 decode at KV32768
-in us/call and HBM GB/s.
+(benchmark config 4) in us/call and HBM GB/s.
 
 Every launch inside the timed region is bracketed by its own pair of events on
 the launching stream, so the roofline's kernel duration is the mean over the
@@ -56,7 +56,7 @@ def parse():
     ap.add_argument("--suite", default="headline",
                     choices=("headline", "decode-scan", "grid", "prefill", "static", "scans"),
                     help="headline: the one-line bench contract (default). decode-scan: "
-                         "BASELINE config 4 split scan; grid: config 2 short-Q grid; "
+                         "config 4 split scan; grid: config 2 short-Q grid; "
                          "prefill: Q4096 and Q32768; static: B1H1 static-plan path against "
                          "the automatic split path; scans: all four scan suites")
     ap.add_argument("--out", default=None, help="scan suites: JSONL file for the records "
@@ -155,7 +155,7 @@ def copy_probe():
 
 
 # ---------------------------------------------------------------------------
-# Scan suites: one record per configuration, each
+# Scan suites (benchmark configs 2-4): one record per configuration, each
 # checked against the oracle before it is timed, as the reference benches do
 # (benchmarks/mha/bench_mha_mfu.py:207-220; bench_v7_split_scan.py:88-120;
 # bench_split_breakdown.py:79-96 for the partial / merge components).
