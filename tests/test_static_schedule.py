@@ -208,3 +208,52 @@ def test_fused_static_path_matches_oracle():
             q, k, v, table, lengths, 128, False)
         rtol, atol = O.TOLERANCES[torch.bfloat16]
         torch.testing.assert_close(got.cpu(), expected, rtol=rtol, atol=atol)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16))
+def test_static_c_entries_general_tasks(dtype):
+    """The C entries take any B, H, D and dtype: task t = (b H + h) q_tiles + q tile.
+    A balanced plan over all tasks (cut tiles included), against the oracle."""
+    from fgw_amd import _lib
+    from fgw_amd.operators.mha.kernels.mha_paged_decode_hip import _current_stream
+    from oracle import mha_oracle as O
+    lib = _lib.load()
+    b, sq, h, d, page, width = 2, 300, 3, 64, 32, 24
+    case = ("static_general", b, sq, h, d, page, width)
+    q, k, v, table = O.make_inputs(case, 5, dtype)
+    lengths = torch.tensor([width * page, 517], dtype=torch.int32)
+    k, v = O.poison_unread(k, v, table, lengths, page)
+    q_tiles = (sq + 127) // 128
+    tasks = b * h * q_tiles
+    plan = S.make_plan(tasks * 128, width * page // 128 * 128, 7)
+    segs, offsets = [], [0]
+    for program in plan.programs:
+        segs.extend(program)
+        offsets.append(len(segs))
+    dev = torch.device("cuda", 0)
+    t_segs = torch.tensor(segs, dtype=torch.int32, device=dev)
+    t_off = torch.tensor(offsets, dtype=torch.int32, device=dev)
+    t_mer = torch.tensor(list(plan.merges) or [(-1, -1, -1)], dtype=torch.int32, device=dev)
+    dq, dk, dv, dt, dl = (x.to(dev) for x in (q, k, v, table, lengths))
+    out = torch.empty_like(dq)
+    slots = plan.partial_count
+    parts = torch.empty(max(1, slots) * 128 * d, dtype=torch.float32, device=dev)
+    lse = torch.empty(max(1, slots) * 128, dtype=torch.float32, device=dev)
+    shape = _lib.Shape(b, sq, h, d, k.shape[0], width, page, 0,
+                       _lib.DTYPE_BFLOAT16 if dtype == torch.bfloat16 else _lib.DTYPE_FLOAT16)
+    tens = _lib.Tensors(dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), dt.data_ptr(), dl.data_ptr(),
+                        out.data_ptr(), parts.data_ptr(), lse.data_ptr())
+    sched = _lib.Schedule(t_segs.data_ptr(), t_off.data_ptr(), t_mer.data_ptr(),
+                          len(plan.programs), len(plan.merges), slots, 128)
+    print(f"static C entries: tasks={tasks} {plan.describe()}", flush=True)
+    stream = _current_stream(0)
+    _lib.check(lib.fgw_mha_static_local(ctypes.byref(shape), ctypes.byref(tens),
+                                        ctypes.byref(sched), stream))
+    _lib.check(lib.fgw_mha_static_merge(ctypes.byref(shape), ctypes.byref(tens),
+                                        ctypes.byref(sched), stream))
+    torch.cuda.synchronize()
+    assert plan.merges  # the plan cuts tiles across programs
+    expected = O.chunked_reference(q, k, v, table, lengths, page, False)
+    rtol, atol = O.TOLERANCES[dtype]
+    torch.testing.assert_close(out.cpu(), expected, rtol=rtol, atol=atol)
