@@ -64,6 +64,16 @@ def _check_cache(k_cache, v_cache, block_table, page_size):
         raise ValueError("contiguous inputs on the same GPU required")
 
 
+def _upload_layout(offsets, table, device):
+    """(cu_rows [B + 1], identity table [B, W]) on the device from one upload:
+    a pinned staging copy of both, copied asynchronously on the current stream
+    (pageable uploads would block the host until the stream drains)."""
+    flat = offsets + [page for row in table for page in row]
+    buf = torch.tensor(flat, dtype=torch.int32).pin_memory().to(device, non_blocking=True)
+    b = len(offsets) - 1
+    return buf[:b + 1], buf[b + 1:].view(b, -1)
+
+
 def _launch_pack(k_cache, v_cache, block_table, cu_rows, total_pages, page_size, out_k, out_v):
     n, h, d = k_cache.shape
     b, w = block_table.shape
@@ -92,8 +102,7 @@ def pack_paged_cache(k_cache, v_cache, block_table, lengths, page_size) -> Packe
     lengths = _host_lengths(lengths, b, w * page_size)
     offsets, rows, table = packed_layout(lengths, page_size, w)
     dev = k_cache.device
-    cu_rows = torch.tensor(offsets, dtype=torch.int32, device=dev)
-    dense_table = torch.tensor(table, dtype=torch.int32, device=dev)
+    cu_rows, dense_table = _upload_layout(offsets, table, dev)
     h, d = k_cache.shape[1:]
     out_k = torch.empty((rows, h, d), dtype=k_cache.dtype, device=dev)
     out_v = torch.empty_like(out_k)
