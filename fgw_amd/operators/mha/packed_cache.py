@@ -128,8 +128,7 @@ def build_gather_attention(case, dtype_name, inputs, cube, splits, device_index)
     _check_cache(k, v, table, page)
     lengths = _host_lengths(lengths, b, width * page)
     offsets, rows, dense = packed_layout(lengths, page, width)
-    cu_rows = torch.tensor(offsets, dtype=torch.int32, device=q.device)
-    dense_table = torch.tensor(dense, dtype=torch.int32, device=q.device)
+    cu_rows, dense_table = _upload_layout(offsets, dense, q.device)
     total_pages = offsets[-1] // page
     attention = cube.build_kernel(b, sq, h, d, rows, width, page, causal, dtype_name,
                                   device_index, num_splits=splits)
