@@ -102,6 +102,21 @@ def load() -> ctypes.CDLL:
         return lib
 
 
+def entry_address(name: str) -> int:
+    """Address of a C entry point of the loaded library (for the launch shim)."""
+    return ctypes.cast(getattr(load(), name), c_void_p).value
+
+
+def load_launch_module():
+    """The C++ launch callable type (fgw_amd._launch); raises if it was not built."""
+    try:
+        from fgw_amd import _launch
+    except ImportError as exc:
+        raise RuntimeError("fgw_amd._launch is missing: build it with `python -m fgw_amd.build` "
+                           "(the operator has no other launch path)") from exc
+    return _launch
+
+
 def check(status: int) -> None:
     """Map a C status to the reference's exception types."""
     if status == FGW_MHA_OK:

@@ -1,4 +1,6 @@
-"""Compile the HIP sources under fgw_amd/csrc into fgw_amd/libfgw_mha.so for gfx950.
+"""Compile the HIP sources under fgw_amd/csrc into fgw_amd/libfgw_mha.so for gfx950,
+and the host-only launch shim (csrc/launch_shim.cpp) into the Python module
+fgw_amd._launch.
 
 Every call rebuilds from scratch (objects under fgw_amd/_build). Run directly
 (`python -m fgw_amd.build`) or through __graft_entry__.build().
@@ -11,6 +13,7 @@ import pathlib
 import shutil
 import subprocess
 import sys
+import sysconfig
 
 PACKAGE = pathlib.Path(__file__).resolve().parent
 CSRC = PACKAGE / "csrc"
@@ -48,17 +51,47 @@ def _compile(source: pathlib.Path) -> pathlib.Path:
     return obj
 
 
+SHIM_SOURCE = CSRC / "launch_shim.cpp"
+
+
+def shim_path() -> pathlib.Path:
+    return PACKAGE / ("_launch" + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
+def _build_shim() -> pathlib.Path:
+    """Host-only C++ extension over the C ABI (torch headers for tensors,
+    allocation and the current HIP stream). Built with g++: no device code."""
+    import torch
+    tdir = pathlib.Path(torch.__file__).resolve().parent
+    out = shim_path()
+    tmp = out.with_name(out.name + ".tmp")
+    cmd = ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wno-unused-function",
+           "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
+           f"-I{tdir / 'include'}", f"-I{tdir / 'include' / 'torch' / 'csrc' / 'api' / 'include'}",
+           "-I/opt/rocm/include", f"-I{sysconfig.get_paths()['include']}",
+           str(SHIM_SOURCE), "-o", str(tmp), f"-L{tdir / 'lib'}", f"-Wl,-rpath,{tdir / 'lib'}",
+           "-lc10", "-lc10_hip", "-ltorch_cpu", "-ltorch_python"]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"launch shim build failed:\n{proc.stdout}{proc.stderr}")
+    os.replace(tmp, out)
+    return out
+
+
 def build(jobs: int | None = None, verbose: bool = True) -> pathlib.Path:
-    """Compile all csrc/*.hip and link the shared library; returns its path."""
+    """Compile all csrc/*.hip, link the shared library and build the launch
+    shim; returns the library path."""
     sources = sorted(CSRC.glob("*.hip"))
     if not sources:
         raise RuntimeError(f"no HIP sources under {CSRC}")
     if BUILD.exists():
         shutil.rmtree(BUILD)
     BUILD.mkdir(parents=True)
-    jobs = jobs or min(len(sources), max(1, min(16, os.cpu_count() or 1)))
+    jobs = jobs or min(len(sources) + 1, max(1, min(16, os.cpu_count() or 1)))
     with cf.ThreadPoolExecutor(max_workers=jobs) as pool:
+        shim = pool.submit(_build_shim)
         objects = list(pool.map(_compile, sources))
+        shim_lib = shim.result()
     tmp = LIBRARY.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-o", str(tmp), *map(str, objects)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
@@ -66,7 +99,7 @@ def build(jobs: int | None = None, verbose: bool = True) -> pathlib.Path:
         raise RuntimeError(f"link failed:\n{proc.stdout}{proc.stderr}")
     os.replace(tmp, LIBRARY)
     if verbose:
-        print(f"built {LIBRARY} from {len(sources)} sources", file=sys.stderr)
+        print(f"built {LIBRARY} from {len(sources)} sources and {shim_lib.name}", file=sys.stderr)
     return LIBRARY
 
 

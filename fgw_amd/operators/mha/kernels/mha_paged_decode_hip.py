@@ -81,11 +81,22 @@ def _persistent_request(persistent_programs) -> int:
     return persistent_programs
 
 
-class _Launch:
-    """Launch callable of one static specialisation; see build_kernel."""
+_launch = _lib.load_launch_module()
+
+
+class _Launch(_launch.Launcher):
+    """Launch callable of one static specialisation; see build_kernel.
+
+    A call (q, k_cache, v_cache, block_table, cache_seqlens) -> O runs in C++
+    (fgw_amd._launch.Launcher, fgw_amd/csrc/launch_shim.cpp): the tensor
+    checks with the messages of _check_detail, the output (and split
+    workspace) allocation, and fgw_mha_fwd on the current stream.
+    """
 
     def __init__(self, shape: _lib.Shape, plan: _lib.Plan, device_index: int, dtype: torch.dtype,
                  meta: dict):
+        super().__init__(bytes(shape), bytes(plan), device_index,
+                         _lib.entry_address("fgw_mha_fwd"), _lib.entry_address("fgw_mha_last_error"))
         self._shape = shape
         self._plan = plan
         self._device = torch.device("cuda", device_index)
@@ -94,13 +105,7 @@ class _Launch:
         self._kv_shape = (shape.pool_rows, shape.heads, shape.dim)
         self._meta_shapes = ((shape.batch, shape.width), (shape.batch,))
         self._index = device_index
-        self._sizes = (torch.Size(self._out_shape), torch.Size(self._kv_shape),
-                       torch.Size(self._meta_shapes[0]), torch.Size(self._meta_shapes[1]))
         self._lib = _lib.load()
-        self._fwd = self._lib.fgw_mha_fwd
-        self._shape_ref = ctypes.byref(shape)
-        self._plan_ref = ctypes.byref(plan)
-        self._ws_floats = plan.parts_floats + plan.lse_floats
         self.block_q = plan.rows_per_tile
         self.compute_grid = plan.grid
         self.task_assignment = "contiguous"
@@ -124,20 +129,9 @@ class _Launch:
 
     # -- helpers -----------------------------------------------------------
     def _check(self, q, k, v, table, lengths):
-        """Shape, dtype, device and layout checks of one call; the fast test
-        passes every valid call, _check_detail names the first violation."""
-        qs, kvs, ts, ls = self._sizes
-        dt, idx, i32 = self._dtype, self._index, torch.int32
-        if (q.shape == qs and k.shape == kvs and v.shape == kvs and table.shape == ts
-                and lengths.shape == ls and q.dtype == dt and k.dtype == dt and v.dtype == dt
-                and table.dtype == i32 and lengths.dtype == i32 and q.get_device() == idx
-                and k.get_device() == idx and v.get_device() == idx
-                and table.get_device() == idx and lengths.get_device() == idx
-                and q.is_contiguous() and k.is_contiguous() and v.is_contiguous()
-                and table.is_contiguous() and lengths.is_contiguous()):
-            return
+        """Checks of the component calls (partial); the full call makes the
+        same checks in C++."""
         self._check_detail(q, k, v, table, lengths)
-        raise ValueError("contiguous inputs on the same GPU required")
 
     def _check_detail(self, q, k, v, table, lengths):
         if (tuple(q.shape) != self._out_shape or tuple(k.shape) != self._kv_shape
@@ -163,27 +157,11 @@ class _Launch:
 
     def _workspace(self):
         """Partials then LSE, carved from one allocation."""
-        ws = torch.empty(self._ws_floats, dtype=torch.float32, device=self._device)
+        ws = torch.empty(self._plan.parts_floats + self._plan.lse_floats, dtype=torch.float32,
+                         device=self._device)
         return ws[:self._plan.parts_floats], ws[self._plan.parts_floats:]
 
-    # -- public calls --------------------------------------------------------
-    def __call__(self, q, k, v, table, lengths):
-        self._check(q, k, v, table, lengths)
-        out = torch.empty(self._out_shape, dtype=self._dtype, device=self._device)
-        if self._plan.execution_mode:
-            ws = torch.empty(self._ws_floats, dtype=torch.float32, device=self._device)
-            parts = ws.data_ptr()
-            t = _lib.Tensors(q.data_ptr(), k.data_ptr(), v.data_ptr(), table.data_ptr(),
-                             lengths.data_ptr(), out.data_ptr(), parts,
-                             parts + 4 * self._plan.parts_floats)
-        else:
-            t = _lib.Tensors(q.data_ptr(), k.data_ptr(), v.data_ptr(), table.data_ptr(),
-                             lengths.data_ptr(), out.data_ptr())
-        rc = self._fwd(self._shape_ref, self._plan_ref, ctypes.byref(t), self._stream())
-        if rc:
-            _lib.check(rc)
-        return out
-
+    # -- component calls -----------------------------------------------------
     def _direct(self, q, k, v, table, lengths):
         return self(q, k, v, table, lengths)
 
@@ -214,6 +192,19 @@ class _Launch:
 
 
 @lru_cache(maxsize=128)
+def _planned(batch, sq, heads, dim, pool_rows, width, page_size, causal, name, device_index,
+             splits, persistent, layout, meta):
+    """Launch callable of one (static shape, split request, grid request,
+    layout): the unit the plan depends on. Ragged lengths reach the cost model
+    before this cache, so a decode step with new lengths re-plans nothing
+    unless the chosen split count changes."""
+    device = _device_info(device_index)
+    shape = _lib.Shape(batch, sq, heads, dim, pool_rows, width, page_size, int(bool(causal)),
+                       _lib.DTYPE_BFLOAT16 if name == "bfloat16" else _lib.DTYPE_FLOAT16)
+    plan = _lib.plan(shape, _lib.Request(splits, persistent, _LAYOUTS[layout]), device)
+    return _Launch(shape, plan, device_index, _DTYPES[name], dict(meta))
+
+
 def build_kernel(batch, sq, heads, dim, pool_rows, width, page_size, causal, dtype,
                  device_index=None, num_splits=None, split_policy="auto", full_kv_cache=False,
                  persistent_programs=PERSISTENT_DEVICE, cache_lengths=None, layout=None):
@@ -228,7 +219,10 @@ def build_kernel(batch, sq, heads, dim, pool_rows, width, page_size, causal, dty
     alternate matrix and softmax phases, D in (32, 128]; "key" = waves split
     key blocks; None: key for Sq <= 32; prefill when its 256-row tiles fill
     the device, or, with KV splits, from Sq 1024, for D in (32, 128]; else
-    query).
+    query). The reference caches build_kernel on its static arguments
+    (lru_cache(128), v7.py:32); here the split count is chosen first (the
+    cost model reads cache_lengths only under the auto/cost_model policy)
+    and the plans are cached per (shape, split count, grid, layout).
     """
     requested_split_policy = split_policy
     if split_policy not in SPLIT_POLICIES:
@@ -244,9 +238,7 @@ def build_kernel(batch, sq, heads, dim, pool_rows, width, page_size, causal, dty
         raise ValueError("positive Q extents and rank-2 table required")
     if device_index is None:
         device_index = torch.cuda.current_device()
-    device = _device_info(int(device_index))
-    shape = _lib.Shape(batch, sq, heads, dim, pool_rows, width, page_size, int(bool(causal)),
-                       _lib.DTYPE_BFLOAT16 if name == "bfloat16" else _lib.DTYPE_FLOAT16)
+    device_index = int(device_index)
     persistent = _persistent_request(persistent_programs)
     if layout not in _LAYOUTS:
         raise ValueError("layout must be None, 'query', 'key' or 'prefill'")
@@ -255,10 +247,11 @@ def build_kernel(batch, sq, heads, dim, pool_rows, width, page_size, causal, dty
         splits, policy = num_splits, "explicit"
     else:
         if split_policy == "auto":
-            use_model = split_cost_model.eligible_config(
+            device = _device_info(device_index)
+            use_model = layout is None and split_cost_model.eligible_config(
                 batch, sq, heads, dim, width * page_size, page_size=page_size, causal=causal,
                 full_kv_cache=full_kv_cache, num_cus=device.num_cus,
-                lengths_known=cache_lengths is not None)
+                lengths_known=cache_lengths is not None, wg_per_cu=tuple(device.wg_per_cu))
             split_policy = "cost_model" if use_model else "legacy"
         if split_policy == "cost_model":
             lengths = cache_lengths
@@ -267,14 +260,14 @@ def build_kernel(batch, sq, heads, dim, pool_rows, width, page_size, causal, dty
                     raise ValueError("Cost model requires full_kv_cache or host-known cache_lengths")
                 lengths = (width * page_size,) * batch
             splits = split_cost_model.select_splits(batch, sq, heads, dim, width * page_size,
-                                                    tuple(lengths), device)
+                                                    tuple(lengths), _device_info(device_index))
         else:
             splits = 0
         policy = split_policy
-    plan = _lib.plan(shape, _lib.Request(splits, persistent, _LAYOUTS[layout]), device)
-    meta = {"persistent_programs": persistent_programs,
-            "requested_split_policy": requested_split_policy, "split_policy": policy}
-    return _Launch(shape, plan, int(device_index), _DTYPES[name], meta)
+    meta = (("persistent_programs", persistent_programs),
+            ("requested_split_policy", requested_split_policy), ("split_policy", policy))
+    return _planned(batch, sq, heads, dim, pool_rows, width, page_size, bool(causal), name,
+                    device_index, splits, persistent, layout, meta)
 
 
 def mha_paged_decode(q, k_cache, v_cache, block_table, cache_seqlens, page_size, is_causal=False,
@@ -306,10 +299,14 @@ def mha_paged_decode(q, k_cache, v_cache, block_table, cache_seqlens, page_size,
     if any(n < 0 or n > capacity for n in lengths):
         raise ValueError("Cache lengths must be within table capacity")
     full_kv_cache = all(n == capacity for n in lengths)
+    # Ragged lengths matter only to the cost model (v7_experimental.py:878-883
+    # forwards them only under that policy); other calls plan without them.
+    wants_lengths = (not full_kv_cache and num_splits is None
+                     and split_policy in ("auto", "cost_model") and not is_causal)
     with torch.cuda.device(q.device):
         kernel = build_kernel(b, sq, h, d, k_cache.shape[0], block_table.shape[1], page_size,
                               bool(is_causal), "float16" if q.dtype == torch.float16 else "bfloat16",
                               q.device.index, num_splits=num_splits, split_policy=split_policy,
                               full_kv_cache=full_kv_cache, persistent_programs=persistent_programs,
-                              cache_lengths=None if full_kv_cache else tuple(lengths))
+                              cache_lengths=tuple(lengths) if wants_lengths else None)
         return kernel(*inputs)

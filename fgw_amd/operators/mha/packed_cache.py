@@ -9,7 +9,8 @@ is one launch of fgw_mha_pack_pages (K and V together, whole pages, zero pages
 for ids outside the pool) and the attention is build_kernel's.
 
 pack_paged_cache is the format step on its own; build_gather_attention keeps
-the reference helper's arguments and returns the same (callable, info) pair.
+the reference helper's arguments and returns a (callable, info) pair, the
+callable a GatherAttention that repacks and attends on every call.
 """
 from __future__ import annotations
 
@@ -88,6 +89,34 @@ def _launch_pack(k_cache, v_cache, block_table, cu_rows, total_pages, page_size,
                                       _current_stream(k_cache.device.index)))
 
 
+class _PackPlan(namedtuple("_PackPlan", "offsets rows cu_rows table total_pages")):
+    """Host offsets, packed rows and the device layout (row offsets, identity
+    table) of one packing of a cache."""
+
+
+def _plan_pack(lengths, page_size, width, device) -> _PackPlan:
+    offsets, rows, table = packed_layout(lengths, page_size, width)
+    cu_rows, dense_table = _upload_layout(offsets, table, device)
+    return _PackPlan(offsets, rows, cu_rows, dense_table, offsets[-1] // page_size)
+
+
+def _pack(k_cache, v_cache, block_table, plan: _PackPlan, page_size):
+    """Dense K/V [rows, H, D] of one packing: one launch moves every live
+    page; rows past the last packed page (only when every length is 0) are
+    zero."""
+    h, d = k_cache.shape[1:]
+    out_k = torch.empty((plan.rows, h, d), dtype=k_cache.dtype, device=k_cache.device)
+    out_v = torch.empty_like(out_k)
+    live = plan.offsets[-1]
+    if live < plan.rows:
+        out_k[live:].zero_()
+        out_v[live:].zero_()
+    if plan.total_pages:
+        _launch_pack(k_cache, v_cache, block_table, plan.cu_rows, plan.total_pages, page_size,
+                     out_k, out_v)
+    return out_k, out_v
+
+
 def pack_paged_cache(k_cache, v_cache, block_table, lengths, page_size) -> PackedCache:
     """Copy every request's live pages, whole and in order, into a dense cache.
 
@@ -100,68 +129,65 @@ def pack_paged_cache(k_cache, v_cache, block_table, lengths, page_size) -> Packe
     _check_cache(k_cache, v_cache, block_table, page_size)
     b, w = block_table.shape
     lengths = _host_lengths(lengths, b, w * page_size)
-    offsets, rows, table = packed_layout(lengths, page_size, w)
-    dev = k_cache.device
-    cu_rows, dense_table = _upload_layout(offsets, table, dev)
-    h, d = k_cache.shape[1:]
-    out_k = torch.empty((rows, h, d), dtype=k_cache.dtype, device=dev)
-    out_v = torch.empty_like(out_k)
-    if offsets[-1] < rows:
-        out_k[offsets[-1]:].zero_()
-        out_v[offsets[-1]:].zero_()
-    _launch_pack(k_cache, v_cache, block_table, cu_rows, offsets[-1] // page_size, page_size,
-                 out_k, out_v)
-    return PackedCache(out_k, out_v, dense_table, cu_rows, offsets, rows)
+    plan = _plan_pack(lengths, page_size, w, k_cache.device)
+    out_k, out_v = _pack(k_cache, v_cache, block_table, plan, page_size)
+    return PackedCache(out_k, out_v, plan.table, plan.cu_rows, plan.offsets, plan.rows)
+
+
+class GatherAttention:
+    """Attention over a packed copy of the live cache, repacked on every call.
+
+    Holds one packing plan (host offsets, device row offsets and identity
+    table, computed once from host lengths) and the launch callable of the
+    attention over the packed pool. A call allocates the dense K/V, packs
+    them in one launch and runs the attention on the original Q with the
+    identity table: the work the reference's packed-cache path times
+    (benchmarks/mha/external_cache_gather.py:66-68). pack() alone returns
+    the dense K/V of a call, for inspection.
+    """
+
+    def __init__(self, q, k, v, table, device_lengths, plan: _PackPlan, page_size, attention):
+        self._inputs = (q, k, v, table, device_lengths)
+        self._plan = plan
+        self._page = page_size
+        self.attention = attention
+        self.packed_rows = plan.offsets[-1]
+        self.rows = plan.rows
+
+    def pack(self):
+        _, k, v, table, _ = self._inputs
+        return _pack(k, v, table, self._plan, self._page)
+
+    def __call__(self):
+        q, _, _, _, device_lengths = self._inputs
+        dense_k, dense_v = self.pack()
+        return self.attention(q, dense_k, dense_v, self._plan.table, device_lengths)
 
 
 def build_gather_attention(case, dtype_name, inputs, cube, splits, device_index):
-    """Pack, check the packed rows exactly, and build attention over the packed cache.
+    """Plan the packing and the attention over the packed cache.
 
-    Arguments as in external_cache_gather.py:14: case = (name, B, Sq, H, D,
+    The arguments and the (callable, info) result are those of the reference
+    helper (external_cache_gather.py:14, :70-77): case = (name, B, Sq, H, D,
     page, width, lengths, causal) with host lengths, inputs = (q, k, v, table,
     device lengths), cube = a module with build_kernel (for example
-    fgw_amd.operators.mha.current). Returns (combined, info): combined() packs
-    K/V (one launch) and runs the attention, the call the reference times.
+    fgw_amd.operators.mha.current). The callable is a GatherAttention. The
+    packed rows are not read back here: a caller that wants them checked
+    compares GatherAttention.pack() with the pool pages itself.
     """
-    name, b, sq, h, d, page, width, lengths, causal = case
+    _, b, sq, h, d, page, width, lengths, causal = case
     q, k, v, table, device_lengths = inputs
     _check_cache(k, v, table, page)
     lengths = _host_lengths(lengths, b, width * page)
-    offsets, rows, dense = packed_layout(lengths, page, width)
-    cu_rows, dense_table = _upload_layout(offsets, dense, q.device)
-    total_pages = offsets[-1] // page
-    attention = cube.build_kernel(b, sq, h, d, rows, width, page, causal, dtype_name,
+    plan = _plan_pack(lengths, page, width, q.device)
+    attention = cube.build_kernel(b, sq, h, d, plan.rows, width, page, causal, dtype_name,
                                   device_index, num_splits=splits)
-
-    def gather_pair():
-        dense_k = torch.empty((rows, h, d), dtype=k.dtype, device=k.device)
-        dense_v = torch.empty_like(dense_k)
-        if offsets[-1]:
-            _launch_pack(k, v, table, cu_rows, total_pages, page, dense_k, dense_v)
-        return dense_k, dense_v
-
-    # Exact check of the packed rows against the original pages
-    # (external_cache_gather.py:55-64), outside the timed call.
-    dense_k, dense_v = gather_pair()
-    table_cpu = table.cpu()
-    for original, packed in ((k, dense_k), (v, dense_v)):
-        original_cpu, packed_cpu = original.cpu(), packed.cpu()
-        for i, n in enumerate(lengths):
-            count = -(-n // page)
-            if count:
-                ids = table_cpu[i, :count].long()
-                expected = original_cpu.view(-1, page, h, d)[ids].reshape(-1, h, d)
-                torch.testing.assert_close(packed_cpu[offsets[i]:offsets[i + 1]], expected,
-                                           rtol=0, atol=0, equal_nan=True)
-
-    def combined():
-        dk, dv = gather_pair()
-        return attention(q, dk, dv, dense_table, device_lengths)
-
-    return combined, {
-        "factory": "fgw_mha_pack_pages", "gather_accuracy": "exact_passed",
-        "gather_calls_per_attention": 1 if offsets[-1] else 0,
-        "packed_rows": offsets[-1], "live_rows": sum(lengths), "num_splits": attention.num_splits,
+    runner = GatherAttention(q, k, v, table, device_lengths, plan, page, attention)
+    return runner, {
+        "factory": "fgw_mha_pack_pages", "gather_accuracy": "unchecked",
+        "gather_calls_per_attention": 1 if plan.total_pages else 0,
+        "packed_rows": plan.offsets[-1], "live_rows": sum(lengths),
+        "num_splits": attention.num_splits,
         "scope": "page-granular pack of K and V in one launch + build_kernel attention",
         "timed": "K/V allocation, one pack launch, all attention/split/merge kernels; "
                  "metadata prepared outside timing",

@@ -37,7 +37,9 @@ FEATURE_NAMES = ("constant", "wave_rounds", "waves", "has_merge", "partial_mbyte
 
 def geometry(sq: int, dim: int = 128):
     """(layout index, rows per tile, keys per round) of the planner's automatic
-    layout choice (fgw_mha_plan: key layout for Sq <= 32, else query layout)."""
+    layout choice inside the model's scope (fgw_mha_plan: key layout for
+    Sq <= 32, else query layout; eligible_config excludes the shapes where the
+    planner takes the prefill layout)."""
     return (1, 32, 128) if sq <= 32 else (0, 128, 64)
 
 
@@ -69,18 +71,34 @@ def load_model(path: str = str(MODEL_PATH)) -> Optional[dict]:
     return model
 
 
+def planner_takes_prefill(batch, sq, heads, dim, num_cus, wg_per_cu) -> bool:
+    """True where fgw_mha_plan's automatic layout is the prefill layout (256-row
+    tiles, fmha_api.hip auto_prefill): head-dim tile 64 or 128, Sq >= 256, and
+    either Sq >= 1024 or its tiles alone fill the device. geometry() does not
+    describe that kernel, so the model is not used there."""
+    dpad = 32
+    while dpad < dim:
+        dpad *= 2
+    if dpad not in (64, 128) or sq < 256:
+        return False
+    wg = max(1, wg_per_cu[2]) if wg_per_cu is not None else 1
+    return sq >= 1024 or batch * heads * math.ceil(sq / 256) >= num_cus * wg
+
+
 def eligible_config(batch, sq, heads, dim, kv_tokens, *, page_size, causal, full_kv_cache,
-                    num_cus, lengths_known=False) -> bool:
+                    num_cus, lengths_known=False, wg_per_cu=None) -> bool:
     """Automatic policy guard: the calibrated scope of the frozen model (non-causal,
-    the calibrated device, table capacity, query length and head dim); the cache
-    lengths must be known on the host (a full cache, or ragged lengths passed in)."""
+    the calibrated device, table capacity, query length and head dim, a layout the
+    features describe); the cache lengths must be known on the host (a full cache,
+    or ragged lengths passed in)."""
     model = load_model()
     if model is None:
         return False
     scope = model["scope"]
     return (not causal and num_cus == scope["num_cus"] and (full_kv_cache or lengths_known)
             and scope["min_kv"] <= kv_tokens <= scope["max_kv"]
-            and scope["min_sq"] <= sq <= scope["max_sq"] and dim in scope["dims"])
+            and scope["min_sq"] <= sq <= scope["max_sq"] and dim in scope["dims"]
+            and not planner_takes_prefill(batch, sq, heads, dim, num_cus, wg_per_cu))
 
 
 def predict(batch, sq, heads, dim, lengths, splits, num_cus, wg_per_cu, model) -> float:

@@ -166,3 +166,35 @@ def test_public_validation_matches_reference_messages():
         build_kernel(1, 1, 2, 16, 32, 2, 16, False, "bfloat16", 0, num_splits=3)
     with pytest.raises(ValueError, match="D must be"):
         build_kernel(1, 1, 2, 24, 32, 2, 16, False, "bfloat16", 0)
+
+
+def test_launch_shim_loads_and_checks_its_arguments(lib):
+    """The C++ launch callable (fgw_amd._launch) loads on the CPU, refuses
+    buffers that are not the C ABI structs, and on a call refuses non-tensors
+    and tensors that do not match its plan with the operator's messages,
+    before any allocation or launch."""
+    launch = _lib.load_launch_module()
+    sh = shape(b=1, sq=4, h=2, d=64, kv=256, page=64)
+    pl = _lib.plan(sh, _lib.Request(1, -1, -1), DEVICE)
+    fwd, err = _lib.entry_address("fgw_mha_fwd"), _lib.entry_address("fgw_mha_last_error")
+    with pytest.raises(TypeError, match="C ABI structs"):
+        launch.Launcher(bytes(sh)[:-4], bytes(pl), 0, fwd, err)
+    with pytest.raises(TypeError, match="function addresses"):
+        launch.Launcher(bytes(sh), bytes(pl), 0, 0, err)
+    call = launch.Launcher(bytes(sh), bytes(pl), 0, fwd, err)
+    q = torch.zeros(1, 4, 2, 64, dtype=torch.bfloat16)
+    kv = torch.zeros(sh.pool_rows, 2, 64, dtype=torch.bfloat16)
+    table = torch.zeros(1, 4, dtype=torch.int32)
+    lengths = torch.zeros(1, dtype=torch.int32)
+    with pytest.raises(TypeError, match="expected"):
+        call(q, kv, kv, table)
+    with pytest.raises(TypeError, match="torch tensors"):
+        call(q, kv, kv, table, 3)
+    with pytest.raises(ValueError, match="tensor shapes"):
+        call(q[:, :3], kv, kv, table, lengths)
+    with pytest.raises(ValueError, match="matching FP16/BF16"):
+        call(q.half(), kv, kv, table, lengths)
+    with pytest.raises(ValueError, match="int32 metadata"):
+        call(q, kv, kv, table.long(), lengths)
+    with pytest.raises(ValueError, match="same GPU"):  # CPU tensors
+        call(q, kv, kv, table, lengths)

@@ -179,27 +179,6 @@ def test_partial_and_merge_components():
         check_output(full, expected, q, lengths, causal, f"components causal={causal}")
 
 
-@pytest.mark.parametrize("dtype", DTYPES)
-def test_decode_split_scan_and_imbalanced(dtype):
-    for sq in (1, 16):
-        for kv in (512, 2048, 8192):
-            for splits in (None, 1, 4, 32):
-                if splits is not None and splits > kv // 32:
-                    continue  # more splits than 32-token KV tiles is rejected
-                case = (f"b2h8_q{sq}_kv{kv}", 2, sq, 8, 128, 128, kv // 128)
-                run_case(case, 7, dtype, False, "full", num_splits=splits)
-    gen = torch.Generator().manual_seed(7)
-    for sq in (1, 16):
-        kv = 8192
-        lengths = torch.randint(kv // 8, kv + 1, (4,), generator=gen).to(torch.int32)
-        q, k, v, table, _ = O.bench_inputs(4, sq, 8, 128, 128, kv, dtype)
-        k, v = O.poison_unread(k, v, table, lengths, 128)
-        from fgw_amd.operators.mha.current import mha_paged_decode
-        got = mha_paged_decode(*(x.cuda() for x in (q, k, v, table, lengths)), page_size=128)
-        expected = O.chunked_reference(q, k, v, table, lengths, 128, False, 128)
-        check_output(got, expected, q, lengths, False, f"imbalanced q{sq}")
-
-
 def test_headline_shapes():
     from fgw_amd.operators.mha.current import build_kernel
     for (b, sq, h, d, p, kv) in ((1, 1, 1, 128, 128, 512), (2, 4096, 8, 128, 128, 2048),

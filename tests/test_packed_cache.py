@@ -102,9 +102,15 @@ def test_gather_attention_matches_paged_attention(name, causal, splits):
     print(f"gather attention {name} causal={causal} splits={splits} lengths={lengths}", flush=True)
     combined, info = P.build_gather_attention(
         (name, b, sq, h, d, p, w, lengths, causal), "bfloat16", inputs, current, splits, 0)
+    assert info["live_rows"] == sum(lengths) and info["packed_rows"] == combined.packed_rows
+    # The packed rows, row-exact against the pool pages (external_cache_gather.py:55-64).
+    dense_k, dense_v = combined.pack()
+    ek, ev, offsets = O.pack_pages(k, v, table, lengths, p)
+    live = offsets[-1]
+    torch.testing.assert_close(dense_k[:live].cpu(), ek[:live], rtol=0, atol=0, equal_nan=True)
+    torch.testing.assert_close(dense_v[:live].cpu(), ev[:live], rtol=0, atol=0, equal_nan=True)
     got = combined()
     torch.cuda.synchronize()
-    assert info["gather_accuracy"] == "exact_passed" and info["live_rows"] == sum(lengths)
     expected = O.reference(q, k, v, table, lt, p, causal)
     rtol, atol = O.TOLERANCES[dtype]
     torch.testing.assert_close(got.cpu(), expected, rtol=rtol, atol=atol)
