@@ -3,16 +3,21 @@
 Headline workload (benchmark config 3): Q4096 / KV2048, B2 H8 D128 BF16,
 page 128, non-causal, full cache, shuffled block table, inputs resident in
 HBM. One step = one call of the launch callable (output allocation and every
-kernel included, compile and H2D excluded), as the reference times it
-(benchmarks/mha/bench_mha_mfu.py:221-247). Alongside: Q1 decode at KV32768
-(benchmark config 4) in us/call and HBM GB/s.
+kernel included, compile and H2D excluded). `value` and `ms_per_step` are the
+reference's statistic (benchmarks/mha/bench_mha_mfu.py:221-240): the median
+of single calls, each bracketed by its own pair of events on the current
+stream and synchronised. Alongside, each figure also back-to-back (one event
+pair around K calls). Companions: Q32768 at the same B/H/KV (config 3) and
+Q1 decode at KV32768 (config 4) in us/call and HBM GB/s.
 
-Every launch inside the timed region is bracketed by its own pair of events on
-the launching stream, so the roofline's kernel duration is the mean over the
-same K launches that give `value`. `traffic` (HBM bytes per launch) comes from
-the rocprofv3 FETCH_SIZE / WRITE_SIZE summary under profiles/, scaled by the
-same counters read for a plain copy of known size (`--copy-probe` is that
-copy).
+`roofline.kernel_us` is the kernel's average launch duration, from the
+back-to-back region (one kernel per direct call; it includes the dispatch gap
+between launches). `traffic` (HBM bytes per launch) comes from the rocprofv3
+FETCH_SIZE / WRITE_SIZE summary under profiles/, scaled by the same counters
+read for a plain copy of known size (`--copy-probe` is that copy).
+
+The CPU baselines time the oracle's torch-fp32 attention (the reference's CPU
+path restated) on this host's cores at 4 threads and at torch's thread count.
 
 Prints one JSON line. `python bench.py --gpus N` with N > 1 exits: the build
 runs on one GPU.
@@ -46,7 +51,6 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--samples", type=int, default=51, help="single-call event samples per workload")
     ap.add_argument("--cpu-threads", type=int, default=0, help="0 = torch's default thread count")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="wall-clock bound of the CPU baseline sample at full thread count")
@@ -449,6 +453,71 @@ def scan_markdown(records):
     return "\n".join(lines) + "\n"
 
 
+def cpu_model() -> str:
+    try:
+        for line in pathlib.Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def gpu_figures(call, steps, warmup, samples):
+    """(single-call median ms, single-call list, back-to-back ms per call)."""
+    import torch
+    for _ in range(warmup):
+        call()
+    torch.cuda.synchronize()
+    single = single_calls(call, samples)
+    back = region_ms(call, steps, 0) / steps
+    return statistics.median(single), single, back
+
+
+def prefill_record(kern, inputs, flops, qkv_bytes, steps, warmup, samples):
+    """Figures of one direct prefill workload; the timed single calls are the step."""
+    med, single, back = gpu_figures(lambda: kern(*inputs), steps, warmup, samples)
+    kernel_ms = back  # direct mode: one kernel per call
+    achieved = flops / (kernel_ms * 1e-3) / 1e12
+    return {
+        "us_per_call": med * 1e3, "us_per_call_min": min(single) * 1e3,
+        "tflops": flops / (med * 1e-3) / 1e12, "mfu_percent": 100.0 * flops / (med * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
+        "us_back_to_back": back * 1e3,
+        "tflops_back_to_back": flops / (back * 1e-3) / 1e12,
+        "grid": kern.compute_grid, "layout": kern.layout, "num_splits": kern.num_splits,
+        "roofline": {"bound": "mfma", "kernel": PREFILL_KERNELS[kern.layout],
+                     "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": achieved / PEAK_BF16_TFLOPS, "kernel_us": kernel_ms * 1e3,
+                     "kernel_us_source": "back-to-back region / calls (HIP events, launch stream)",
+                     "algorithmic_flops": flops, "algorithmic_bytes": qkv_bytes},
+    }
+
+
+def cpu_baselines(host, dhosts, page, flops, threads_full, budget_s):
+    """The oracle's chunked torch-fp32 attention on the host cores: the headline
+    prefill, config 1 and Q1 decode at KV 512 / 2048 / 8192 / 32768, each at 4
+    threads (the reference harness cap) and at the full thread count."""
+    import torch
+    from oracle import mha_oracle as O
+    out = {"cpu_model": cpu_model(), "cores_full": threads_full, "cores_cap": 4}
+    pre = {}
+    for threads, budget in ((threads_full, budget_s), (4, budget_s / 2)):
+        sec, reps, expected = cpu_timed(host, page, threads, budget)
+        pre[threads] = (sec, reps)
+    out["prefill"] = {str(t): {"seconds_per_call": s_, "runs": r, "tflops": flops / s_ / 1e12}
+                      for t, (s_, r) in pre.items()}
+    dec = {}
+    for label, (dh, nbytes) in dhosts.items():
+        row = {}
+        for threads in (4, threads_full):
+            sec, reps, _ = cpu_timed(dh, page, threads, budget_s / 8, min_reps=3)
+            row[str(threads)] = {"us_per_call": sec * 1e6, "runs": reps, "gbs": nbytes / sec / 1e9}
+        dec[label] = row
+    out["decode"] = dec
+    torch.set_num_threads(threads_full)
+    return out, expected
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -468,12 +537,13 @@ def main():
     dev = torch.device("cuda", 0)
     cores = args.cpu_threads or torch.get_num_threads()
     rtol, atol = O.TOLERANCES[torch.bfloat16]
+    b, h, d, page, kv = 2, 8, 128, 128, 2048
 
-    # ---- headline: Q4096 / KV2048 prefill ------------------------------
     # GPU measurements first: the CPU baselines (tens of seconds of host work)
-    # come after them, so that the timed regions do not start on a GPU whose
-    # clocks dropped while it sat idle.
-    b, sq, h, d, page, kv = 2, 4096, 8, 128, 128, 2048
+    # come after them, so that no timed region starts on a GPU whose clocks
+    # dropped while it sat idle.
+    # ---- headline: Q4096 / KV2048 prefill (the step) ---------------------
+    sq = 4096
     host = O.bench_inputs(b, sq, h, d, page, kv, torch.bfloat16)
     inputs = [x.to(dev) for x in host]
     kern = build_kernel(b, sq, h, d, host[1].shape[0], kv // page, page, False, "bfloat16", 0,
@@ -481,14 +551,27 @@ def main():
     flops = O.useful_flops([kv] * b, sq, h, d, False)
     got = kern(*inputs)
     torch.cuda.synchronize()
-    call = lambda: kern(*inputs)  # noqa: E731
-    samples = single_calls(call, args.samples)  # untimed by the region; also warms the clocks
-    total_ms = region_ms(call, args.steps, args.warmup)
-    ms = total_ms / args.steps
-    kernel_ms = ms  # direct mode: one kernel per call
-    tflops = flops / (ms * 1e-3) / 1e12
-    achieved = flops / (kernel_ms * 1e-3) / 1e12
-    qkv_bytes = O.algorithmic_bytes([kv] * b, sq, h, d, kv // page)
+    torch.cuda.synchronize()
+    head = prefill_record(kern, inputs, flops, O.algorithmic_bytes([kv] * b, sq, h, d, kv // page),
+                          args.steps, args.warmup, args.steps)
+    head["roofline"]["traffic"] = traffic_from_profile("prefill_direct")
+    head["roofline"]["traffic_source"] = str(TRAFFIC_SUMMARY.relative_to(ROOT))
+
+    # ---- companion: Q32768 / KV2048 prefill ------------------------------
+    big_sq = 32768
+    bhost = O.bench_inputs(b, big_sq, h, d, page, kv, torch.bfloat16)
+    binputs = [x.to(dev) for x in bhost]
+    bkern = build_kernel(b, big_sq, h, d, bhost[1].shape[0], kv // page, page, False, "bfloat16",
+                         0, full_kv_cache=True)
+    bflops = O.useful_flops([kv] * b, big_sq, h, d, False)
+    bgot = bkern(*binputs)
+    torch.cuda.synchronize()
+    big_steps = max(5, args.steps // 5)
+    big = prefill_record(bkern, binputs, bflops,
+                         O.algorithmic_bytes([kv] * b, big_sq, h, d, kv // page),
+                         big_steps, max(2, args.warmup // 5), big_steps)
+    big["workload"] = "Q32768/KV2048 B2H8 D128 BF16 page128 non-causal full cache"
+    big["steps"] = big_steps
 
     # ---- decode: Q1 / KV32768 -------------------------------------------
     db, dsq, dkv = 2, 1, 32768
@@ -499,63 +582,80 @@ def main():
     dgot = dkern(*dinputs)
     torch.cuda.synchronize()
     dbytes = O.algorithmic_bytes([dkv] * db, dsq, h, d, dkv // page)
-    dcall = lambda: dkern(*dinputs)  # noqa: E731
-    d_samples = single_calls(dcall, args.samples)
-    d_total = region_ms(dcall, args.steps, args.warmup)
-    d_us = statistics.median(d_samples) * 1e3
-    decode = {"workload": "Q1/KV32768 B2H8 D128 BF16 page128", "us_per_call": d_us,
-              "gbs": dbytes / (d_us * 1e-6) / 1e9,
-              "us_per_call_back_to_back": d_total / args.steps * 1e3,
-              "bytes": dbytes, "num_splits": dkern.num_splits, "split_policy": dkern.split_policy,
-              "grid": dkern.compute_grid, "execution_mode": dkern.execution_mode}
+    d_med, d_single, d_back = gpu_figures(lambda: dkern(*dinputs), args.steps, args.warmup,
+                                          args.steps)
+    decode = {"workload": "Q1/KV32768 B2H8 D128 BF16 page128", "us_per_call": d_med * 1e3,
+              "us_per_call_min": min(d_single) * 1e3, "gbs": dbytes / (d_med * 1e-3) / 1e9,
+              "us_back_to_back": d_back * 1e3, "bytes": dbytes, "num_splits": dkern.num_splits,
+              "split_policy": dkern.split_policy, "grid": dkern.compute_grid,
+              "execution_mode": dkern.execution_mode,
+              "roofline_call": {"bound": "hbm", "kernel": "whole call (every kernel, single-call "
+                                "median)", "achieved": dbytes / (d_med * 1e-3) / 1e9,
+                                "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                                "frac": dbytes / (d_med * 1e-3) / 1e9 / PEAK_HBM_GBS}}
     if dkern.execution_mode == "split_and_merge":
         pcall = lambda: dkern.partial_kernel(*dinputs)  # noqa: E731
         p_ms = region_ms(pcall, args.steps, args.warmup) / args.steps
         p_achieved = dbytes / (p_ms * 1e-3) / 1e9
-        p_traffic = traffic_from_profile("decode_partial")
         decode["roofline"] = {"bound": "hbm", "kernel": "fwd_kernel (partial, key layout)",
                               "achieved": p_achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                              "frac": p_achieved / PEAK_HBM_GBS, "traffic": p_traffic,
-                              "kernel_us": p_ms * 1e3}
+                              "frac": p_achieved / PEAK_HBM_GBS,
+                              "traffic": traffic_from_profile("decode_partial"),
+                              "traffic_source": str(TRAFFIC_SUMMARY.relative_to(ROOT)),
+                              "kernel_us": p_ms * 1e3,
+                              "kernel_us_source": "back-to-back region of partial-only calls / calls"}
 
-    # ---- correctness of both workloads and the CPU baselines -------------
+    # ---- correctness of every workload, then the CPU baselines ----------
+    dsmall = {}
+    for dk in (512, 2048, 8192):
+        dh = O.bench_inputs(db, dsq, h, d, page, dk, torch.bfloat16)
+        dsmall[f"Q1/KV{dk} B2H8"] = (dh, O.algorithmic_bytes([dk] * db, dsq, h, d, dk // page))
+    dsmall["Q1/KV32768 B2H8"] = (dhost, dbytes)
+    c1 = O.bench_inputs(1, 1, 1, 128, page, 512, torch.bfloat16)
+    dsmall["config1 B1H1 Q1/KV512"] = (c1, O.algorithmic_bytes([512], 1, 1, 128, 512 // page))
     cpu = None
     if not args.no_cpu_baseline:
-        cpu_s, reps, expected = cpu_timed(host, page, cores, args.cpu_seconds)
-        cpu4_s, reps4, _ = cpu_timed(host, page, 4, args.cpu_seconds / 2)
-        cpu = {"value": flops / cpu_s / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
+        base, expected = cpu_baselines(host, dsmall, page, flops, cores, args.cpu_seconds)
+        full = base["prefill"][str(cores)]
+        cpu = {"value": full["tflops"], "unit": "TFLOP/s", "cores": cores, "kind": "port",
+               "cpu_model": base["cpu_model"],
                "sample": f"whole Q4096/KV2048 B2H8 D128 workload, oracle chunked_reference "
-                         f"(torch fp32, chunk 128), median of {reps} runs at "
-                         f"torch.set_num_threads({cores}); value_4_threads: median of {reps4} runs "
-                         f"at 4 threads (the reference harness cap)",
-               "seconds_per_call": cpu_s, "value_4_threads": flops / cpu4_s / 1e12}
+                         f"(torch fp32, chunk 128), median of {full['runs']} runs at "
+                         f"torch.set_num_threads({cores}); value_4_threads at 4 threads (the "
+                         "reference harness cap); decode: Q1 at KV 512/2048/8192/32768 and "
+                         "config 1, each at 4 and full threads",
+               "seconds_per_call": full["seconds_per_call"],
+               "value_4_threads": base["prefill"]["4"]["tflops"],
+               "decode": base["decode"]}
     else:
         expected = O.chunked_reference(*host, page, False, 128)
     torch.testing.assert_close(got.cpu(), expected, rtol=rtol, atol=atol)
     dexp = O.chunked_reference(*dhost, page, False, 128)
     torch.testing.assert_close(dgot.cpu(), dexp, rtol=rtol, atol=atol)
-    if not args.no_cpu_baseline:
-        c_s, creps, _ = cpu_timed(dhost, page, cores, args.cpu_seconds / 4, min_reps=3)
-        decode["cpu_baseline"] = {"value": dbytes / c_s / 1e9, "unit": "GB/s", "cores": cores,
-                                  "kind": "port",
-                                  "sample": f"whole Q1/KV32768 workload, median of {creps} runs"}
+    # Q32768: every query row of both requests' first 256-row tile and last tile
+    # against the oracle (the whole oracle would take minutes on the host).
+    rows = list(range(256)) + list(range(big_sq - 256, big_sq))
+    bexp = O.chunked_reference(bhost[0][:, rows], *bhost[1:], page, False, 128)
+    torch.testing.assert_close(bgot[:, rows].cpu(), bexp, rtol=rtol, atol=atol)
 
     line = {
-        "metric": METRIC, "value": tflops, "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "metric": METRIC, "value": head["tflops"], "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": head["us_per_call"] / 1e3,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic",
+        "statistic": "median of single calls, each between its own event pair and synchronised "
+                     "(bench_mha_mfu.py:221-240)",
         "config": {"workload": "Q4096/KV2048 B2H8 D128 BF16 page128 non-causal full cache",
                    "batch": b, "q_len": sq, "kv_len": kv, "heads": h, "head_dim": d,
-                   "page_size": page, "num_splits": kern.num_splits, "grid": kern.compute_grid,
-                   "layout": kern.layout},
-        "mfu_percent": 100.0 * tflops / PEAK_BF16_TFLOPS,
-        "median_single_call_us": statistics.median(samples) * 1e3,
-        "roofline": {"bound": "mfma", "kernel": PREFILL_KERNELS[kern.layout],
-                     "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": achieved / PEAK_BF16_TFLOPS,
-                     "traffic": traffic_from_profile("prefill_direct"),
-                     "algorithmic_bytes": qkv_bytes, "kernel_us": kernel_ms * 1e3},
+                   "page_size": page, "num_splits": head["num_splits"], "grid": head["grid"],
+                   "layout": head["layout"]},
+        "mfu_percent": head["mfu_percent"],
+        "us_per_call_min": head["us_per_call_min"],
+        "us_back_to_back": head["us_back_to_back"],
+        "tflops_back_to_back": head["tflops_back_to_back"],
+        "roofline": head["roofline"],
         "cpu_baseline": cpu,
+        "q32768": big,
         "decode": decode,
     }
     print(json.dumps(line), flush=True)
