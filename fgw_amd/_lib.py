@@ -10,9 +10,10 @@ import pathlib
 import threading
 
 LIBRARY = pathlib.Path(__file__).resolve().with_name("libfgw_mha.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 FGW_MHA_OK, FGW_MHA_EINVAL, FGW_MHA_EUNSUPPORTED, FGW_MHA_EHIP = 0, -1, -2, -3
+NOALLOC_SCRATCH_BYTES = 32 << 20  # FGW_MHA_NOALLOC_SCRATCH_BYTES
 DTYPE_FLOAT16, DTYPE_BFLOAT16 = 0, 1
 LAYOUT_AUTO, LAYOUT_QUERY, LAYOUT_KEY, LAYOUT_PREFILL = -1, 0, 1, 2
 NUM_LAYOUTS = 3
@@ -62,6 +63,8 @@ SIGNATURES = {
     "fgw_mha_plan": (ctypes.POINTER(Shape), ctypes.POINTER(Request), ctypes.POINTER(DeviceInfo),
                      ctypes.POINTER(Plan)),
     "fgw_mha_fwd": (ctypes.POINTER(Shape), ctypes.POINTER(Plan), ctypes.POINTER(Tensors), c_void_p),
+    "fgw_mha_fwd_noalloc": (ctypes.POINTER(Shape), ctypes.POINTER(Plan),
+                            ctypes.POINTER(Tensors), c_void_p),
     "fgw_mha_partial": (ctypes.POINTER(Shape), ctypes.POINTER(Plan), ctypes.POINTER(Tensors),
                         c_void_p),
     "fgw_mha_merge": (ctypes.POINTER(Shape), ctypes.POINTER(Plan), ctypes.POINTER(Tensors),

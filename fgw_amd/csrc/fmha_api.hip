@@ -6,6 +6,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 
 #include "../../include/fgw_mha.h"
 #include "fmha_aux.h"
@@ -99,6 +100,41 @@ int hip_fail(hipError_t e, const char* what) {
 constexpr int kMaxSplits = 128;
 constexpr int kAutoMaxSplits = 64;
 constexpr int kMinRoundsPerSplit = 2;
+
+// Split workspace of fgw_mha_fwd_noalloc: partials then LSE of one call, in
+// a device array the code object brings (each GPU that loads the library
+// holds its own copy until the process ends). Host code never passes the
+// array's name to a kernel: that is a host-side stand-in, not a device
+// address. It uses the address hipGetSymbolAddress returns on each device.
+constexpr int64_t kScratchFloats = FGW_MHA_NOALLOC_SCRATCH_BYTES / 4;
+static __device__ __align__(256) float scratch[kScratchFloats];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+float* g_scratch_ptr[kMaxDevices] = {};
+
+// This device's address of `scratch`, looked up once per device with that
+// device current (the caller's current device is restored).
+int scratch_address(int device, float** out) {
+  if (device < 0 || device >= kMaxDevices)
+    return fail(FGW_MHA_EUNSUPPORTED, "device %d is outside the scratch table", device);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[device]) {
+    int current = 0;
+    hipError_t err = hipGetDevice(&current);
+    if (err != hipSuccess) return hip_fail(err, "hipGetDevice");
+    if (current != device && (err = hipSetDevice(device)) != hipSuccess)
+      return hip_fail(err, "hipSetDevice");
+    void* ptr = nullptr;
+    err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (current != device) (void)hipSetDevice(current);
+    if (err != hipSuccess) return hip_fail(err, "hipGetSymbolAddress(scratch)");
+    if (!ptr) return fail(FGW_MHA_EHIP, "hipGetSymbolAddress(scratch) returned NULL");
+    g_scratch_ptr[device] = static_cast<float*>(ptr);
+  }
+  *out = g_scratch_ptr[device];
+  return FGW_MHA_OK;
+}
 
 // Keys one program consumes per loop round, and query rows per work item,
 // per layout.
@@ -379,6 +415,33 @@ int fgw_mha_fwd(const fgw_mha_shape* s, const fgw_mha_plan_t* p, const fgw_mha_t
   rc = launch_partial_kernel(s, p, t, 1, stream);
   if (rc) return rc;
   return launch_merge_kernel(s, p, t, stream);
+}
+
+int fgw_mha_fwd_noalloc(const fgw_mha_shape* s, const fgw_mha_plan_t* p,
+                        const fgw_mha_tensors* t, hipStream_t stream) {
+  int rc = check_shape(s);
+  if (!rc) rc = check_plan(s, p);
+  if (!rc) rc = check_tensors(t, true, true, false);
+  if (rc) return rc;
+  if (p->num_splits == 1) return launch_partial_kernel(s, p, t, 0, stream);
+  const int64_t need = p->parts_floats + p->lse_floats;
+  if (need > kScratchFloats)
+    return fail(FGW_MHA_EUNSUPPORTED,
+                "split workspace of %lld bytes exceeds the %lld-byte static scratch of "
+                "fgw_mha_fwd_noalloc; use fgw_mha_fwd with a caller workspace",
+                (long long)need * 4, (long long)kScratchFloats * 4);
+  int device = 0;
+  hipError_t err = stream ? hipStreamGetDevice(stream, &device) : hipGetDevice(&device);
+  if (err != hipSuccess) return hip_fail(err, "stream device");
+  float* base = nullptr;
+  rc = scratch_address(device, &base);
+  if (rc) return rc;
+  fgw_mha_tensors w = *t;
+  w.parts = base;  // 256-byte aligned
+  w.lse = base + p->parts_floats;
+  rc = launch_partial_kernel(s, p, &w, 1, stream);
+  if (rc) return rc;
+  return launch_merge_kernel(s, p, &w, stream);
 }
 
 int fgw_mha_partial(const fgw_mha_shape* s, const fgw_mha_plan_t* p, const fgw_mha_tensors* t,

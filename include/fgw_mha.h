@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define FGW_MHA_ABI_VERSION 2
+#define FGW_MHA_ABI_VERSION 3
 
 typedef enum {
   FGW_MHA_OK = 0,
@@ -144,6 +144,25 @@ int fgw_mha_plan(const fgw_mha_shape* shape, const fgw_mha_request* request,
  * launch callable returned by build_kernel (v7.py:471-473, :495-498). */
 int fgw_mha_fwd(const fgw_mha_shape* shape, const fgw_mha_plan_t* plan,
                 const fgw_mha_tensors* t, hipStream_t stream);
+
+/* Bytes of the static device scratch that fgw_mha_fwd_noalloc uses as its
+ * split workspace (partials then LSE, parts_floats + lse_floats fp32). */
+#define FGW_MHA_NOALLOC_SCRATCH_BYTES (32ll << 20)
+
+/* fgw_mha_fwd without a caller workspace and without any allocation: the
+ * split workspace (t->parts / t->lse are ignored and may be NULL) is a static
+ * device array of FGW_MHA_NOALLOC_SCRATCH_BYTES that the library holds on
+ * every GPU it runs on until the process ends; its device address is looked
+ * up once per device (on the device of `stream`). No reference counterpart:
+ * for callers that cannot allocate device memory (HIP graph capture, serving
+ * loops, harnesses that forbid hipMalloc). Plans whose parts_floats +
+ * lse_floats exceed the scratch are rejected (FGW_MHA_EUNSUPPORTED). Direct
+ * plans (num_splits == 1) need no scratch. Every call on one GPU shares that
+ * GPU's scratch: calls that overlap on one GPU (other streams, other host
+ * threads) race on it. Nothing in it needs clearing: the partial kernel
+ * writes every row the merge reads. */
+int fgw_mha_fwd_noalloc(const fgw_mha_shape* shape, const fgw_mha_plan_t* plan,
+                        const fgw_mha_tensors* t, hipStream_t stream);
 
 /* Partial kernel only: writes parts[b,h,s,q,:] = O_s / l_s and lse[b,h,s,q].
  * Replaces launch.partial_kernel (v7.py:225-315, :488-490), the component the
