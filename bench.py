@@ -226,15 +226,16 @@ def suite_decode_scan(args, emit):
                             kern, dinputs, args.scan_samples, args.scan_warmup)
                     emit(rec)
         # Imbalanced variant: B4, lengths uniform in [KV/8, KV] (seeded), width KV/page.
-        for sq in (1, 16):
-            kv = 8192
-            lengths = torch.randint(kv // 8, kv + 1, (4,), generator=torch.Generator().manual_seed(7))
+        for sq, kv in ((sq, kv) for sq in (1, 16) for kv in (512, 2048, 8192, 32768)):
+            lengths = O.imbalanced_lengths(kv)
             q, k, v, table, _ = O.bench_inputs(4, sq, h, d, page, kv, dtype)
-            host = (q, k, v, table, lengths.to(torch.int32))
+            host = (q, k, v, table, lengths)
             dinputs = [x.to(dev) for x in host]
             expected = O.chunked_reference(*host, page, False, 128)
             nbytes = O.algorithmic_bytes(lengths.tolist(), sq, h, d, kv // page)
             for req in (None, 1, 4, 16):
+                if req is not None and req > kv // 32:
+                    continue
                 kern = build_kernel(4, sq, h, d, k.shape[0], kv // page, page, False,
                                     "bfloat16" if name == "bf16" else "float16", 0,
                                     num_splits=req)

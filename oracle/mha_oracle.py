@@ -229,6 +229,14 @@ def bench_inputs(b, sq, h, d, page_size, length, dtype, seed=7):
     return q, k, v, table, lengths
 
 
+def imbalanced_lengths(length, batch=4, seed=7):
+    """Benchmark config 4's imbalanced decode variant: per-request lengths drawn
+    uniformly in [length / 8, length] from Generator().manual_seed(seed) (one
+    randint draw, int32); the table width stays length / page."""
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(length // 8, length + 1, (batch,), generator=g).to(torch.int32)
+
+
 def gather_packed(k, v, table, lengths, page_size, out_len):
     """Packed [B, out_len, H, D] copies of each request's live rows, zero past len."""
     b = table.shape[0]

@@ -93,8 +93,7 @@ def test_config4_imbalanced_b4(dtype, kv):
     width KV / page; through the public entry (automatic split from the
     host-known ragged lengths) and at forced splits."""
     from fgw_amd.operators.mha.current import build_kernel, mha_paged_decode
-    lengths = torch.randint(kv // 8, kv + 1, (4,),
-                            generator=torch.Generator().manual_seed(7)).to(torch.int32)
+    lengths = O.imbalanced_lengths(kv)
     for sq in (1, 16):
         q, k, v, table, _ = O.bench_inputs(4, sq, 8, 128, 128, kv, dtype)
         k, v = O.poison_unread(k, v, table, lengths, 128)

@@ -266,3 +266,33 @@ def test_bench_inputs_recipe_properties():
     assert all(torch.equal(a, b) for a, b in zip((q, k, v, table), again[:4]))
     other = O.bench_inputs(2, 3, 4, 16, 8, 40, torch.bfloat16, seed=8)
     assert not torch.equal(table, other[3]) or not torch.equal(q, other[0])
+
+
+def test_bench_inputs_recipe_values():
+    """Literal values of the benchmark recipe at seed 7 (B2, Q4096, H8, D128,
+    page 128, KV 2048): the shuffled table and the first draws of q, k and v.
+    They fail an unshuffled (identity) table, a different seed and a changed
+    draw order (table, then q, k, v; bench_mha_mfu.py:181-187). The
+    reference records none of these values, so they pin the recipe against
+    changes of this restatement, not against a reference run."""
+    q, k, v, table, lengths = O.bench_inputs(2, 4096, 8, 128, 128, 2048, torch.bfloat16)
+    assert table.tolist() == [[15, 11, 3, 6, 19, 20, 21, 1, 12, 16, 30, 24, 5, 22, 9, 29],
+                              [26, 7, 27, 10, 8, 18, 2, 23, 28, 13, 31, 0, 4, 14, 25, 17]]
+    assert not torch.equal(table.flatten(), torch.arange(32, dtype=torch.int32))
+    assert q[0, 0, 0, :4].float().tolist() == [0.50390625, -0.08349609375, -0.0234375,
+                                               0.1748046875]
+    assert k[0, 0, :4].float().tolist() == [0.59375, 1.2578125, 0.75, -0.88671875]
+    assert v[-1, -1, -4:].float().tolist() == [1.7578125, -1.6875, 0.4296875, -0.404296875]
+
+
+def test_imbalanced_lengths_recipe():
+    """Config 4's imbalanced variant, randint(KV // 8, KV + 1, (4,)) from
+    Generator().manual_seed(7), at every KV of the config: literal values, and
+    every length inside [KV / 8, KV]."""
+    expected = {512: [415, 147, 348, 469], 2048: [1194, 1931, 345, 1618],
+                8192: [4635, 4285, 4326, 1917], 32768: [13321, 16319, 6592, 12115]}
+    for kv, want in expected.items():
+        got = O.imbalanced_lengths(kv)
+        assert got.dtype == torch.int32 and got.tolist() == want
+        assert all(kv // 8 <= n <= kv for n in want)
+    assert O.imbalanced_lengths(8192, seed=8).tolist() != expected[8192]
