@@ -2,7 +2,7 @@
 //
 // A work item is (b, h, 256-row query tile, KV split). Eight waves own 32
 // query rows each and share every 64-key K/V block, which the DMA engine
-// moves from HBM into a three-slot K ring and a four-slot V ring in LDS.
+// moves from HBM into four-slot K and V rings in LDS.
 // Per block a wave computes S^T = K . Q^T and O^T += V^T . P^T on
 // v_mfma_f32_32x32x16 with the operand layouts and the online softmax of
 // fwd_kernel (fmha_kernel.h; reference math: operators/mha/kernels/
@@ -23,25 +23,30 @@
 //   phase 2m:      A: M(m)        B: S(m - 1)   all: DMA batch of block m + 2
 //   phase 2m + 1:  A: S(m)        B: M(m)       all: wait for block m + 1
 //
-// for m = 0 .. N (N blocks). M(0) runs the PV of "block -1" with P = 0 over
-// a zero-filled V slot, M(N) a QK^T of a clamped block whose scores are
-// never used, so every M phase runs the same code. S(n) rescales O after the
-// PV of block n - 1 (in M(n)) and before that of block n (in M(n + 1)).
+// for m = 0 .. N (N blocks). M(0) has no PV (there is no block -1) and M(N)
+// no QK^T (there is no block N); both loops peel them. S(n) rescales O
+// after the PV of block n - 1 (in M(n)) and before that of block n (in
+// M(n + 1)).
 //
-// DMA. Block j's K and V tiles go to K slot j % 3 and V slot j % 4; the
+// DMA. Block j's K and V tiles go to K slot j % 4 and V slot j % 4; the
 // batch of block j (clamped to N - 1) is issued in phase 2(j - 2) by every
-// wave (its share of the tile's 1 KB instructions). The K slot held block
-// j - 3, last read in phase 2j - 5; the V slot block j - 4, last read in
-// phase 2j - 5. The wait at the end of phase 2m + 1 leaves only the batch
-// of block m + 2 in flight, so block m + 1 (K read from phase 2m + 2) has
-// landed; V of block m was waited for a pair earlier. The pool offset of
-// block j comes from a 64-block window of per-lane offsets (one table read
-// per lane every 64 blocks) by readlane. The loads are issued by inline
-// assembly: the compiler then neither sees them as LDS writes (it would
-// otherwise wait for every outstanding DMA before each transposing LDS
-// read) nor counts them; the explicit waits here are the only ones they
-// need, and the compiler's own vmcnt waits stay correct because loads
-// retire in order.
+// wave (its share of the tile's 1 KB instructions). Both slots held block
+// j - 4, last read in phase 2j - 7 (K) and 2j - 5 (V). The wait at the end
+// of phase 2m + 1 leaves only the batch of block m + 2 in flight, so block
+// m + 1 (K read from phase 2m + 2) has landed; V of block m was waited for
+// a pair earlier. The pool offset of block j comes from a 64-block window of
+// per-lane offsets (one table read per lane every 64 blocks) by readlane.
+// The loads are issued by inline assembly: the compiler then neither sees
+// them as LDS writes (it would otherwise wait for every outstanding DMA
+// before each transposing LDS read) nor counts them; the explicit waits here
+// are the only ones they need, and the compiler's own vmcnt waits stay
+// correct because loads retire in order.
+//
+// Operand addresses. Each lane keeps the LDS address of its K operand for
+// every k-step (the K chunks are XOR-swizzled per row, so the eight differ
+// per lane) and the base of its V^T reads; a matrix phase adds the ring
+// slot once per k-step, and every other part of an address (S^T tile, PV
+// k-step) is an immediate offset of the LDS read.
 #pragma once
 #include <utility>
 
@@ -81,7 +86,7 @@ struct PCfg {
   static constexpr int CPR = DPAD / 8;  // 16-byte chunks per LDS row
   static constexpr int ROW_BYTES = DPAD * 2;
   static constexpr int TILE_BYTES = BN * ROW_BYTES;
-  static constexpr int NKSLOT = 3;
+  static constexpr int NKSLOT = 4;
   static constexpr int NVSLOT = 4;
   static constexpr int LDS_BYTES = (NKSLOT + NVSLOT) * TILE_BYTES;
   static constexpr int INSTR = TILE_BYTES / 1024;  // DMA instructions per tile
@@ -91,6 +96,7 @@ struct PCfg {
   static constexpr int VSW = CPR / 4;
   static constexpr int RPI = 64 / CPR;
   static_assert(DPAD == 64 || DPAD == 128, "prefill layout head-dim tiles");
+  static_assert(NKSLOT == 4 && NVSLOT == 4, "matrix phases take slots n % 4");
   static_assert(INSTR % NWQ == 0 && INSTR_PER_WAVE >= 1, "DMA granularity");
   static_assert(LDS_BYTES <= kLdsBudget, "LDS budget of one CU");
 };
@@ -169,30 +175,65 @@ __device__ __forceinline__ void issue_fast_block(const char* kbase, const char* 
   }
 }
 
-// Matrix phase of one wave: O^T += V^T P^T over the V tile `vt` (the
-// previous block), then S^T = K Q^T over the K tile `kt`. One sequence of
-// DT KS + ST KK MFMAs, each operand read from LDS AH operands ahead.
+// Per-lane LDS byte addresses of the MFMA A operands, ring bases included:
+//   K (k-step kk):  kring + k_base + 32 (kk ^ ky)          (+ slot, + 32 t rows)
+//   V (O^T tile dt): vring + v_base + 64 (dt ^ vy)         (+ slot, + 16 k2 rows)
+// The slot and row parts are compile-time constants of the matrix phase, so
+// every operand read is one of these registers plus an immediate offset.
 template <class C>
-__device__ __forceinline__ void matrix_phase(const unsigned char* kt, const unsigned char* vt,
-                                             const Lanes<C>& ln, const u32x4 (&qf)[C::KK],
+struct OperandAddr {
+  u32 k[C::KK];
+  u32 v;  // vring + v_base
+  int vy;
+  __device__ __forceinline__ OperandAddr(const Lanes<C>& ln, u32 kring, u32 vring) {
+#pragma unroll
+    for (int kk = 0; kk < C::KK; ++kk) k[kk] = kring + (u32)(ln.k_base + 32 * (kk ^ ln.ky));
+    v = vring + (u32)ln.v_base;
+    vy = ln.vy;
+  }
+};
+
+typedef __attribute__((address_space(3))) unsigned char lds_byte;
+
+__device__ __forceinline__ lds_byte* lds_at(u32 addr) { return (lds_byte*)(uintptr_t)addr; }
+
+// Matrix phase of one wave with block n's K tile in K slot KSLOT and block
+// n - 1's V tile in V slot (KSLOT + 3) % 4: O^T += V^T P^T, then S^T = K Q^T.
+// One sequence of DT KS + ST KK MFMAs, each operand read from LDS AH
+// operands ahead.
+template <class C, bool PV, bool QK>
+__device__ __forceinline__ void matrix_phase(const OperandAddr<C>& ad, u32 koff, u32 voff,
+                                             const u32x4 (&qf)[C::KK],
                                              const u32x4 (&pf)[C::KS], f32x16 (&s)[C::ST],
                                              f32x16 (&o)[C::DT]) {
   using E = Elem<C::BF16>;
-  constexpr int NPV = C::DT * C::KS, NQK = C::ST * C::KK, NOP = NPV + NQK;
-  constexpr int AH = 7;
+  // Operand i of the sequence: PV steps first (when PV), then QK^T steps (when QK).
+  constexpr int NPV = PV ? C::DT * C::KS : 0, NQK = QK ? C::ST * C::KK : 0, NOP = NPV + NQK;
+  constexpr int AH = NOP < 7 ? NOP : 7;
   // Operand i: PV step (k2 = i / DT, dt = i % DT) for i < NPV, else QK^T step
   // (kk = (i - NPV) / ST, t = (i - NPV) % ST).
   auto rd = [&](auto ic) -> u32x4 {
     constexpr int i = decltype(ic)::value;
-    if constexpr (i < NPV)
-      return read_vt<C>(vt, ln, i % C::DT, i / C::DT);
-    else
-      return read_k<C>(kt, ln, (i - NPV) % C::ST, (i - NPV) / C::ST);
+    if constexpr (i < NPV) {
+      constexpr int dt = i % C::DT, k2 = i / C::DT;
+      lds_byte* va = lds_at(ad.v + 64 * (dt ^ ad.vy) + voff) + 16 * k2 * C::ROW_BYTES;
+      const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)va);
+      const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) i16x4*)(va + 8 * C::ROW_BYTES));
+      const u32x2 lo2 = __builtin_bit_cast(u32x2, lo), hi2 = __builtin_bit_cast(u32x2, hi);
+      return u32x4{lo2.x, lo2.y, hi2.x, hi2.y};
+    } else {
+      constexpr int t = (i - NPV) % C::ST, kk = (i - NPV) / C::ST;
+      return *(const __attribute__((address_space(3))) u32x4*)(lds_at(ad.k[kk] + koff) +
+                                                               t * 32 * C::ROW_BYTES);
+    }
   };
+  if constexpr (QK) {
 #pragma unroll
-  for (int t = 0; t < C::ST; ++t)
+    for (int t = 0; t < C::ST; ++t)
 #pragma unroll
-    for (int v = 0; v < 16; ++v) s[t][v] = 0.0f;
+      for (int v = 0; v < 16; ++v) s[t][v] = 0.0f;
+  }
   u32x4 a[AH + 1];
   // The wave of the SIMD that runs the softmax would otherwise take every
   // VALU issue cycle it can and hold back these MFMAs; at the higher
@@ -290,7 +331,7 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p,
       // following window is read one window ahead.
       BlockWindow win0{0, block_offset<C>(p, table_b, row_bytes, key0, N, len, lane)};
       BlockWindow win1{1, 0};
-      // K and V of block j (clamped to N - 1) into K slot j % 3, V slot j % 4.
+      // K and V of block j (clamped to N - 1) into K slot j % 4, V slot j % 4.
       auto issue_block = [&](int j) {
         const int jc = j < N ? j : N - 1;
         if ((jc >> 6) != win0.w) {  // uniform: the block entered the next window
@@ -327,10 +368,6 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p,
         }
       }
       win1.off = block_offset<C>(p, table_b, row_bytes, key0, N, len, 64 + lane);
-      // V slot 3 holds "block -1", read by the PV of M(0) with P = 0.
-      for (int i = tid * 16; i < C::TILE_BYTES; i += C::THREADS * 16)
-        *reinterpret_cast<u32x4*>(vring + (C::NVSLOT - 1) * C::TILE_BYTES + i) =
-            u32x4{0u, 0u, 0u, 0u};
       wait_vm<C::BATCH>();  // block 0
       // Q has landed too (its loads are younger than block 0's). The empty
       // assembly makes the compiler wait for them here, once, instead of
@@ -342,15 +379,17 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p,
 
       f32x16 s[C::ST];
       u32x4 pf[C::KS];
-#pragma unroll
-      for (int k2 = 0; k2 < C::KS; ++k2) pf[k2] = u32x4{0u, 0u, 0u, 0u};
 
-      // M(n): PV of block n - 1 (V slot (n + 3) % 4), QK^T of block n (K slot n % 3).
-      auto mphase = [&](int n) {
-        matrix_phase<C>(kring + (n % C::NKSLOT) * C::TILE_BYTES,
-                        vring + ((n + C::NVSLOT - 1) % C::NVSLOT) * C::TILE_BYTES, ln, qf, pf, s,
-                        o);
+      // M(n): PV of block n - 1 (V slot (n + 3) % 4), QK^T of block n (K slot
+      // n % 4); M(0) skips the PV and M(N) the QK^T.
+      const OperandAddr<C> ad(ln, kring_lds, vring_lds);
+      auto mphase = [&](int n, auto pv, auto qk) {
+        const u32 ks = (u32)((n & 3) * C::TILE_BYTES);
+        const u32 vs = (u32)(((n + 3) & 3) * C::TILE_BYTES);
+        matrix_phase<C, decltype(pv)::value, decltype(qk)::value>(ad, ks, vs, qf, pf, s, o);
       };
+      constexpr std::true_type on{};
+      constexpr std::false_type off{};
       // S(n): softmax of block n.
       auto sphase = [&](int n) {
         const int pos0 = key0 + n * C::BN;
@@ -362,35 +401,48 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p,
       // block n + 2 at the start of phase 2n and, at the end of phase
       // 2n + 1, waits until only that batch may be in flight (block n + 1
       // has landed). Straight-line loops per group keep the register
-      // assignment of O, S and P fixed across phases.
+      // assignment of O, S and P fixed across phases; each group passes
+      // 2N + 2 barriers.
       if (group_a) {
-        for (int n = 0; n < N; ++n) {
+        issue_block(2);
+        mphase(0, off, on);
+        __syncthreads();
+        sphase(0);
+        wait_vm<C::BATCH>();
+        __syncthreads();
+        for (int n = 1; n < N; ++n) {
           issue_block(n + 2);
-          mphase(n);
+          mphase(n, on, on);
           __syncthreads();
           sphase(n);
           wait_vm<C::BATCH>();
           __syncthreads();
         }
         issue_block(N + 2);
-        mphase(N);
+        mphase(N, on, off);
         __syncthreads();
         wait_vm<C::BATCH>();
         __syncthreads();
       } else {
         issue_block(2);
         __syncthreads();
-        mphase(0);
+        mphase(0, off, on);
         wait_vm<C::BATCH>();
         __syncthreads();
-        for (int n = 1; n <= N; ++n) {
+        for (int n = 1; n < N; ++n) {
           issue_block(n + 2);
           sphase(n - 1);
           __syncthreads();
-          mphase(n);
+          mphase(n, on, on);
           wait_vm<C::BATCH>();
           __syncthreads();
         }
+        issue_block(N + 2);
+        sphase(N - 1);
+        __syncthreads();
+        mphase(N, on, off);
+        wait_vm<C::BATCH>();
+        __syncthreads();
       }
       wait_vm<0>();  // no DMA of this work item outlives it
     }
