@@ -555,6 +555,14 @@ __device__ __forceinline__ float lse_of(float m_log2, float total) {
   return total > 0.0f ? (m_log2 + log2f(total)) * kLn2 : kNegBig;
 }
 
+// floor(nblk * s / splits): the first key block of split s (0 <= s <= splits
+// <= 128). 32-bit arithmetic whenever the product fits, which avoids the
+// 64-bit division routine.
+__device__ __forceinline__ int split_bound(int nblk, int s, int splits) {
+  if (nblk < (1 << 24)) return (int)(((u32)nblk * (u32)s) / (u32)splits);
+  return (int)((int64_t)nblk * s / splits);
+}
+
 // Page id of the page holding logical position pos.
 __device__ __forceinline__ int32_t page_id(const FwdParams& p, const int32_t* table_b, int pos) {
   return table_b[div_page((u32)pos, p.page_magic, p.page_shift)];
@@ -617,6 +625,18 @@ __global__ __launch_bounds__(C::THREADS) void fwd_kernel(FwdParams p,
     const char* kb = static_cast<const char*>(p.k) + (int64_t)h * p.dim * 2;
     const char* vb = static_cast<const char*>(p.v) + (int64_t)h * p.dim * 2;
 
+    // Page ids of this wave's first two key blocks for a full cache, read
+    // together with the length instead of after it; a shorter length moves
+    // the block range and they are read again below.
+    constexpr int kStep = C::NWK * C::BN;
+    int spec_pos = -1;
+    int32_t spec0 = 0, spec1 = 0;
+    if (p.mode != 2 && !p.causal) {
+      const int nfull = (capacity + C::BN - 1) / C::BN;
+      spec_pos = (split_bound(nfull, split, p.splits) + wk) * C::BN;
+      if (spec_pos < capacity) spec0 = page_id(p, table_b, spec_pos);
+      if (spec_pos + kStep < capacity) spec1 = page_id(p, table_b, spec_pos + kStep);
+    }
     int len = lengths[b];
     len = len < 0 ? 0 : (len > capacity ? capacity : len);
     const int q0 = qt * C::ROWS_TILE;
@@ -629,8 +649,8 @@ __global__ __launch_bounds__(C::THREADS) void fwd_kernel(FwdParams p,
       blk_end = seg_hi < nblk ? seg_hi : nblk;
       blk_begin = seg_lo < blk_end ? seg_lo : blk_end;
     } else {
-      blk_begin = (int)((int64_t)nblk * split / p.splits);
-      blk_end = (int)((int64_t)nblk * (split + 1) / p.splits);
+      blk_begin = split_bound(nblk, split, p.splits);
+      blk_end = split_bound(nblk, split + 1, p.splits);
     }
     const int cnt = blk_end - blk_begin;
     const int my_n = cnt > wk ? (cnt - wk + C::NWK - 1) / C::NWK : 0;
@@ -644,6 +664,28 @@ __global__ __launch_bounds__(C::THREADS) void fwd_kernel(FwdParams p,
     int vis = p.causal ? len - p.sq + qrow + 1 : len;
     vis = vis < 0 ? 0 : (vis > len ? len : vis);
 
+    float m = kNegBig, l = 0.0f;
+    f32x16 o[C::DT];
+#pragma unroll
+    for (int dt = 0; dt < C::DT; ++dt)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) o[dt][v] = 0.0f;
+
+    const int first_pos = (blk_begin + wk) * C::BN;
+    const bool spec = first_pos == spec_pos;
+    if (it > 0) __syncthreads();  // LDS of the previous work item is no longer read
+    // Every key group streams its blocks n = 0, 1, ... at key
+    // (blk_begin + wk + NWK n) * BN through its own LDS stages; the DMA of
+    // block n + 1 is in flight while block n is computed.
+    int32_t next_id = my_n > 1 ? (spec ? spec1 : page_id(p, table_b, first_pos + kStep)) : 0;
+    if (my_n > 0) {
+      const int32_t id0 = spec ? spec0 : page_id(p, table_b, first_pos);
+      issue_tile<C, false>(p, dl, table_b, kb, row_bytes, first_pos, id0, len, group_base, wq,
+                           lane);
+      issue_tile<C, true>(p, dl, table_b, vb, row_bytes, first_pos, id0, len,
+                          group_base + C::TILE_BYTES, wq, lane);
+    }
+    // Q after the first DMA: its loads overlap the tile's.
     u32x4 qf[C::KK];
     {
       const u16* qp =
@@ -655,27 +697,6 @@ __global__ __launch_bounds__(C::THREADS) void fwd_kernel(FwdParams p,
         if (qrow < p.sq && d < p.dim) val = load16(qp + d);
         qf[kk] = val;
       }
-    }
-    float m = kNegBig, l = 0.0f;
-    f32x16 o[C::DT];
-#pragma unroll
-    for (int dt = 0; dt < C::DT; ++dt)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) o[dt][v] = 0.0f;
-
-    constexpr int kStep = C::NWK * C::BN;
-    const int first_pos = (blk_begin + wk) * C::BN;
-    __syncthreads();  // LDS of the previous work item is no longer read
-    // Every key group streams its blocks n = 0, 1, ... at key
-    // (blk_begin + wk + NWK n) * BN through its own LDS stages; the DMA of
-    // block n + 1 is in flight while block n is computed.
-    int32_t next_id = my_n > 1 ? page_id(p, table_b, first_pos + kStep) : 0;
-    if (my_n > 0) {
-      const int32_t id0 = page_id(p, table_b, first_pos);
-      issue_tile<C, false>(p, dl, table_b, kb, row_bytes, first_pos, id0, len, group_base, wq,
-                           lane);
-      issue_tile<C, true>(p, dl, table_b, vb, row_bytes, first_pos, id0, len,
-                          group_base + C::TILE_BYTES, wq, lane);
     }
     for (int n = 0; n < my_n; ++n) {
       const int pos0 = first_pos + kStep * n;
