@@ -44,6 +44,15 @@ FwdEntry fwd_entry(bool bf16, int dpad, int layout) {
 }
 
 hipError_t launch_merge(bool bf16, const MergeParams& p, hipStream_t stream) {
+  if (p.splits > kMergeChunk) {  // splits spread over a workgroup per row
+    const dim3 grid((unsigned)((int64_t)p.batch * p.heads * p.sq));
+    if (bf16) {
+      merge_wide_kernel<true><<<grid, dim3(kMergeThreads), 0, stream>>>(p);
+    } else {
+      merge_wide_kernel<false><<<grid, dim3(kMergeThreads), 0, stream>>>(p);
+    }
+    return hipGetLastError();
+  }
   // One (row, 4 dims) pair per thread: a workgroup covers whole rows.
   const int rows_per_wg = (4 * kMergeThreads) / p.dim > 0 ? (4 * kMergeThreads) / p.dim : 1;
   const int64_t groups = (p.sq + rows_per_wg - 1) / rows_per_wg;

@@ -84,6 +84,89 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(MergeParams p, int
                    bh % p.heads, q0, rows, threadIdx.x, kMergeThreads);
 }
 
+// LSE merge of one output row (b, h, q) per workgroup with the splits spread
+// over the threads, for split counts above kMergeChunk (where merge_one
+// would take one memory round trip per chunk). Thread (g, c), g < G =
+// kMergeThreads / (D / 4), takes dims 4c .. 4c + 3 of splits g, g + G, ...
+// and folds them as merge_one does (running peak per chunk of kMergeChunk,
+// weights exp(LSE - peak), empty splits weight 0) without normalising; the
+// G group states are then rescaled to the common peak and summed in group
+// order through LDS, and O = acc / max(tot, 1e-30) is cast to the input
+// dtype. An all-empty row is exactly zero.
+template <bool BF16>
+__global__ __launch_bounds__(kMergeThreads) void merge_wide_kernel(MergeParams p) {
+  using E = Elem<BF16>;
+  __shared__ float speak[kMergeThreads];
+  __shared__ float stot[kMergeThreads];
+  __shared__ f32x4 sacc[kMergeThreads];
+  const int d4n = p.dim / 4;
+  const int G = kMergeThreads / d4n;
+  const int t = threadIdx.x, c = t % d4n, g = t / d4n;
+  const bool act = g < G;
+  const int q = (int)(blockIdx.x % (unsigned)p.sq);
+  const int bh = (int)(blockIdx.x / (unsigned)p.sq);
+  const int b = bh / p.heads, h = bh % p.heads;
+  const int64_t base = (int64_t)bh * p.splits * p.sq + q;  // (b, h, split 0, q)
+  const float* ls = p.lse + base;
+  const float* ps = p.parts + base * p.dim + 4 * c;
+  const int64_t part_stride = (int64_t)p.sq * p.dim;
+  float peak = kNegBig, tot = 0.0f;
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (act) {
+    for (int s0 = g; s0 < p.splits; s0 += kMergeChunk * G) {
+      float x[kMergeChunk];
+      f32x4 v[kMergeChunk];
+#pragma unroll
+      for (int i = 0; i < kMergeChunk; ++i) {
+        const int s = s0 + i * G < p.splits ? s0 + i * G : g;  // clamped; weight 0 below
+        x[i] = ls[(int64_t)s * p.sq];
+        v[i] = *reinterpret_cast<const f32x4*>(ps + (int64_t)s * part_stride);
+      }
+      float cpeak = peak;
+#pragma unroll
+      for (int i = 0; i < kMergeChunk; ++i) {
+        const bool live = s0 + i * G < p.splits && x[i] > -1.0e29f;
+        cpeak = live ? fmaxf(cpeak, x[i]) : cpeak;
+      }
+      const float keep = expf(peak - cpeak);
+      tot *= keep;
+      acc *= keep;
+#pragma unroll
+      for (int i = 0; i < kMergeChunk; ++i) {
+        const bool live = s0 + i * G < p.splits && x[i] > -1.0e29f;
+        const float wgt = live ? expf(x[i] - cpeak) : 0.0f;
+        tot += wgt;
+        acc += live ? v[i] * wgt : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+      peak = cpeak;
+    }
+    if (c == 0) speak[g] = peak;  // the same in every thread of the group
+  }
+  __syncthreads();
+  float top = kNegBig;
+  for (int k = 0; k < G; ++k) top = fmaxf(top, speak[k]);
+  if (act) {
+    const float scale = expf(peak - top);  // 0 for an empty group below a live peak
+    sacc[t] = acc * scale;
+    if (c == 0) stot[g] = tot * scale;
+  }
+  __syncthreads();
+  if (g == 0) {
+    f32x4 a = {0.0f, 0.0f, 0.0f, 0.0f};
+    float total = 0.0f;
+    for (int k = 0; k < G; ++k) {
+      a += sacc[k * d4n + c];
+      total += stot[k];
+    }
+    const float inv = 1.0f / fmaxf(total, 1.0e-30f);
+    u32x2 w;
+    w.x = E::pack2(a[0] * inv, a[1] * inv);
+    w.y = E::pack2(a[2] * inv, a[3] * inv);
+    u16* dst = static_cast<u16*>(p.out) + (((int64_t)b * p.sq + q) * p.heads + h) * p.dim + 4 * c;
+    *reinterpret_cast<u32x2*>(dst) = w;
+  }
+}
+
 // Merge of the static schedule's split tiles: group g (task, first slot,
 // slots) is merged by groups_wg workgroups, workgroup j taking rows
 // [j rows_wg, (j + 1) rows_wg) of the tile; the partials of slot s are in

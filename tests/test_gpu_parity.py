@@ -179,6 +179,34 @@ def test_partial_and_merge_components():
         check_output(full, expected, q, lengths, causal, f"components causal={causal}")
 
 
+def test_wide_merge_many_splits():
+    """Merges of more than 16 splits (the splits spread over one workgroup per
+    row) against the oracle merge: head dims whose column count does not divide
+    the workgroup (48), several chunks per thread (D 256, 128 splits), empty
+    splits and one all-empty row (exact zero)."""
+    from fgw_amd.operators.mha.current import build_kernel
+    gen = torch.Generator().manual_seed(11)
+    cases = ((2, 3, 2, 128, 64, torch.bfloat16), (1, 1, 3, 48, 128, torch.float16),
+             (2, 2, 1, 256, 32, torch.bfloat16), (1, 5, 2, 16, 32, torch.float16),
+             (2, 1, 8, 128, 32, torch.bfloat16), (1, 2, 1, 256, 128, torch.bfloat16))
+    for (b, sq, h, d, splits, dtype) in cases:
+        page, kv = 32, splits * 64
+        name = "bfloat16" if dtype == torch.bfloat16 else "float16"
+        kern = build_kernel(b, sq, h, d, b * kv, kv // page, page, False, name, 0,
+                            num_splits=splits)
+        assert kern.num_splits == splits and kern.execution_mode == "split_and_merge"
+        parts = torch.randn(b, h, splits, sq, d, generator=gen)
+        lse = torch.randn(b, h, splits, sq, generator=gen) * 4.0
+        lse[torch.rand(lse.shape, generator=gen) < 0.3] = -1e30
+        lse[0, 0, :, 0] = -1e30
+        out = kern.merge_kernel(parts.cuda(), lse.cuda())
+        torch.cuda.synchronize()
+        label = f"wide merge B{b} Q{sq} H{h} D{d} splits={splits} {name}"
+        assert torch.equal(out[0, 0, 0].cpu(), torch.zeros(d, dtype=dtype)), label
+        torch.testing.assert_close(out.cpu().float(), O.merge_partials(parts, lse, dtype).float(),
+                                   rtol=8e-3, atol=1e-5, msg=label)
+
+
 def test_headline_shapes():
     from fgw_amd.operators.mha.current import build_kernel
     for (b, sq, h, d, p, kv) in ((1, 1, 1, 128, 128, 512), (2, 4096, 8, 128, 128, 2048),
