@@ -65,6 +65,9 @@ def parse():
                          "the automatic split path; scans: all four scan suites")
     ap.add_argument("--out", default=None, help="scan suites: JSONL file for the records "
                     "(a markdown summary is written beside it)")
+    ap.add_argument("--grid-splits", action="store_true",
+                    help="grid suite: every admissible split count 1..128 besides split 1 and "
+                         "auto (calibration data for the split cost model)")
     ap.add_argument("--scan-samples", type=int, default=21)
     ap.add_argument("--scan-warmup", type=int, default=5)
     return ap.parse_args()
@@ -196,7 +199,7 @@ def _checked(kern, dinputs, expected, dtype, label):
 
 def suite_decode_scan(args, emit):
     """Config 4: B2 H8 D128 page 128, Q in {1, 16} x KV in {512 .. 32768}, FP16 and
-    BF16, splits 1..32 and auto; plus the imbalanced B4 variant."""
+    BF16, splits 1..64 and auto; plus the imbalanced B4 variant."""
     import torch
     from fgw_amd.operators.mha.current import build_kernel
     from oracle import mha_oracle as O
@@ -209,7 +212,7 @@ def suite_decode_scan(args, emit):
                 dinputs = [x.to(dev) for x in host]
                 expected = O.chunked_reference(*host, page, False, 128)
                 nbytes = O.algorithmic_bytes([kv] * b, sq, h, d, kv // page)
-                for req in (None, 1, 2, 4, 8, 16, 32):
+                for req in (None, 1, 2, 4, 8, 16, 32, 64):
                     if req is not None and req > kv // 32:
                         continue
                     kern = build_kernel(b, sq, h, d, host[1].shape[0], kv // page, page, False,
@@ -254,7 +257,8 @@ def suite_decode_scan(args, emit):
 
 def suite_grid(args, emit):
     """Config 2: B1 H1 D128 BF16 page 128, Q in {1 .. 512} x KV in {128 .. 16384};
-    each spec as one direct kernel (split 1) and with the automatic split."""
+    each spec as one direct kernel (split 1) and with the automatic split, and with
+    --grid-splits at every split count 2..128 the planner admits."""
     import torch
     from fgw_amd.operators.mha.current import build_kernel
     from oracle import mha_oracle as O
@@ -265,9 +269,13 @@ def suite_grid(args, emit):
             dinputs = [x.to(dev) for x in host]
             expected = O.chunked_reference(*host, 128, False, 128)
             flops = O.useful_flops([kv], sq, 1, 128, False)
-            for req in (1, None):
-                kern = build_kernel(1, sq, 1, 128, host[1].shape[0], kv // 128, 128, False,
-                                    "bfloat16", 0, num_splits=req, full_kv_cache=True)
+            reqs = (1, None) + ((2, 4, 8, 16, 32, 64, 128) if args.grid_splits else ())
+            for req in reqs:
+                try:
+                    kern = build_kernel(1, sq, 1, 128, host[1].shape[0], kv // 128, 128, False,
+                                        "bfloat16", 0, num_splits=req, full_kv_cache=True)
+                except ValueError:  # more splits than key blocks
+                    continue
                 _checked(kern, dinputs, expected, torch.bfloat16, f"grid q{sq} kv{kv} {req}")
                 single, back = _time_call(lambda: kern(*dinputs), args.scan_samples,
                                           args.scan_warmup)

@@ -11,7 +11,9 @@ several split counts) the score differences between candidates should match
 the latency differences, weighted by 1 / best latency of the case, with
 nonnegative weights. Case-constant costs cancel, so the constant feature gets
 weight 0 and scores rank candidates rather than predict absolute latency.
-Solved here with scipy's nonnegative least squares on the stacked differences.
+Solved here with scipy's nonnegative least squares on the stacked differences,
+with the weight of the partial-bytes feature chosen on a grid by the in-sample
+selection quality (least squares alone leaves it at zero; see fit()).
 
     python -m fgw_amd.operators.mha.fit_split_cost_model SCAN.jsonl [SCAN2.jsonl ...]
 
@@ -75,7 +77,7 @@ def load_cases(paths) -> tuple:
     return [c for c in cases.values() if len(c["lat"]) >= 2], _Device(*device)
 
 
-def fit(cases, device) -> List[float]:
+def _differences(cases, device):
     rows, target = [], []
     for c in cases:
         best = min(c["lat"].values())
@@ -89,11 +91,41 @@ def fit(cases, device) -> List[float]:
                                     device.num_cus, device.wg_per_cu))
             rows.append((f - f0) / best)
             target.append((t - c["lat"][base_s]) / best)
-    a, y = np.array(rows), np.array(target)
+    return np.array(rows), np.array(target)
+
+
+def _nnls(a, y) -> np.ndarray:
     scale = np.linalg.norm(a, axis=0)
     scale[scale == 0] = 1.0
     w, _ = nnls(a / scale, y)
-    return (w / scale).tolist()
+    return w / scale
+
+
+# Grid of the partial-bytes weight (us per MB of fp32 partials written and read
+# back): 0 .. 0.3, i.e. down to ~6.7 TB/s for the round trip.
+PARTIAL_MB_GRID = tuple(round(0.01 * i, 2) for i in range(31))
+
+
+def fit(cases, device, tolerance: float = 0.03, margin: float = 0.5) -> List[float]:
+    """Weights of split_cost_model.features. The partial-bytes weight is taken
+    from PARTIAL_MB_GRID by the in-sample selection quality (geomean, then worst
+    selected/best ratio, then residual); given it, the others are the
+    nonnegative least squares solution. Least squares alone leaves that
+    weight at 0: the few long-query cases where partial traffic decides the
+    choice carry little of the squared error."""
+    a, y = _differences(cases, device)
+    col = M.FEATURE_NAMES.index("partial_mbytes")
+    rest = np.delete(a, col, axis=1)
+    best_key, best_w = None, None
+    for pm in PARTIAL_MB_GRID:
+        w = np.insert(_nnls(rest, y - a[:, col] * pm), col, pm)
+        rep = evaluate(w.tolist(), cases, device, tolerance, margin)
+        residual = float(np.linalg.norm(a @ w - y))
+        key = (round(rep["geomean_relative_to_best"], 6), round(rep["max_relative_to_best"], 6),
+               residual)
+        if best_key is None or key < best_key:
+            best_key, best_w = key, w
+    return best_w.tolist()
 
 
 def evaluate(weights, cases, device, tolerance, margin) -> dict:
@@ -131,7 +163,7 @@ def main(argv=None) -> int:
     ap.add_argument("--margin-us", type=float, default=0.5)
     args = ap.parse_args(argv)
     cases, device = load_cases(args.scans)
-    weights = fit(cases, device)
+    weights = fit(cases, device, args.tolerance, args.margin_us)
     report = evaluate(weights, cases, device, args.tolerance, args.margin_us)
     lens = [c["capacity"] for c in cases]
     sqs = [c["sq"] for c in cases]
@@ -151,7 +183,8 @@ def main(argv=None) -> int:
                      "sha256": hashlib.sha256(pathlib.Path(p).read_bytes()).hexdigest()}
                     for p in args.scans],
         "fit": "nonnegative least squares on within-case latency differences against the "
-               "smallest scanned split, weighted by 1 / best latency of the case",
+               "smallest scanned split, weighted by 1 / best latency of the case; the "
+               "partial-bytes weight searched on a grid by in-sample selection quality",
     }
     pathlib.Path(args.output).write_text(json.dumps(model, indent=2) + "\n")
     print(json.dumps({k: v for k, v in model.items() if k not in ("sources",)}, indent=2))

@@ -30,7 +30,7 @@ from functools import lru_cache
 from typing import Optional, Sequence
 
 MODEL_PATH = pathlib.Path(__file__).with_name("split_cost_model.json")
-SPLITS = (1, 2, 4, 8, 16, 32, 64)
+SPLITS = (1, 2, 4, 8, 16, 32, 64, 128)
 FEATURE_NAMES = ("constant", "wave_rounds", "waves", "has_merge", "partial_mbytes", "merge_rows",
                  "longest_excess")
 
