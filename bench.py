@@ -58,11 +58,14 @@ def parse():
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 1 GiB device copy (counter calibration) and exit")
     ap.add_argument("--suite", default="headline",
-                    choices=("headline", "decode-scan", "grid", "prefill", "static", "scans"),
+                    choices=("headline", "decode-scan", "grid", "prefill", "static", "power",
+                             "scans"),
                     help="headline: the one-line bench contract (default). decode-scan: "
                          "config 4 split scan; grid: config 2 short-Q grid; "
                          "prefill: Q4096 and Q32768; static: B1H1 static-plan path against "
-                         "the automatic split path; scans: all four scan suites")
+                         "the automatic split path; power: MFMA rate on N(0,1) against "
+                         "constant inputs (library GEMM and the headline kernel); scans: the "
+                         "first four scan suites")
     ap.add_argument("--out", default=None, help="scan suites: JSONL file for the records "
                     "(a markdown summary is written beside it)")
     ap.add_argument("--grid-splits", action="store_true",
@@ -380,11 +383,50 @@ def suite_static(args, emit):
               "speedup": t_auto / t_static})
 
 
+def suite_power(args, emit):
+    """Data dependence of the MFMA rate (power-limited shader clock): a library
+    bf16 GEMM (torch.matmul, 8192^3) and the headline prefill kernel, each on
+    N(0,1) inputs and on constant inputs (every element 1/8 in bf16), timed
+    back to back with one event pair."""
+    import torch
+    from fgw_amd.operators.mha.current import build_kernel
+    from oracle import mha_oracle as O
+    dev = torch.device("cuda", 0)
+    n = 8192
+    gen = torch.Generator(device=dev).manual_seed(7)
+    for data in ("normal", "constant"):
+        if data == "normal":
+            a = torch.randn(n, n, device=dev, generator=gen).to(torch.bfloat16)
+            bm = torch.randn(n, n, device=dev, generator=gen).to(torch.bfloat16)
+        else:
+            a = torch.full((n, n), 0.125, device=dev, dtype=torch.bfloat16)
+            bm = torch.full((n, n), 0.125, device=dev, dtype=torch.bfloat16)
+        steps = 20
+        ms = region_ms(lambda: torch.matmul(a, bm), steps, 5)
+        emit({"suite": "power", "workload": "torch.matmul bf16 8192^3", "data": data,
+              "us_per_call": ms / steps * 1e3, "tflops": 2 * n ** 3 / (ms / steps * 1e-3) / 1e12})
+        del a, bm
+    b, sq, h, d, page, kv = 2, 4096, 8, 128, 128, 2048
+    host = O.bench_inputs(b, sq, h, d, page, kv, torch.bfloat16)
+    kern = build_kernel(b, sq, h, d, host[1].shape[0], kv // page, page, False, "bfloat16", 0,
+                        full_kv_cache=True)
+    flops = O.useful_flops([kv] * b, sq, h, d, False)
+    for data in ("normal", "constant"):
+        dinputs = [x.to(dev) for x in host]
+        if data == "constant":
+            for x in dinputs[:3]:
+                x.fill_(0.125)
+        steps = 100
+        ms = region_ms(lambda: kern(*dinputs), steps, 20)
+        emit({"suite": "power", "workload": "prefill Q4096/KV2048 B2H8 D128 BF16", "data": data,
+              "us_per_call": ms / steps * 1e3, "tflops": flops / (ms / steps * 1e-3) / 1e12})
+
+
 def run_scans(args):
     import torch
     torch.cuda.set_device(0)
     suites = {"decode-scan": [suite_decode_scan], "grid": [suite_grid],
-              "prefill": [suite_prefill], "static": [suite_static],
+              "prefill": [suite_prefill], "static": [suite_static], "power": [suite_power],
               "scans": [suite_prefill, suite_decode_scan, suite_grid, suite_static]}[args.suite]
     out = open(args.out, "w") if args.out else None
     records = []
@@ -412,6 +454,13 @@ def run_scans(args):
 def scan_markdown(records):
     """Summary tables of the scan records (the figures quoted in the docs)."""
     lines = []
+    pw = [r for r in records if r["suite"] == "power"]
+    if pw:
+        lines += ["## MFMA rate against input data (back-to-back, one event pair)", "",
+                  "| workload | data | us/call | TFLOP/s |", "|---|---|---|---|"]
+        lines += [f"| {r['workload']} | {r['data']} | {r['us_per_call']:.1f} | {r['tflops']:.0f} |"
+                  for r in pw]
+        lines.append("")
     st = [r for r in records if r["suite"] == "static"]
     if st:
         lines += ["## Static plan vs automatic split (B1H1 D128 BF16, full page-128 KV, "
