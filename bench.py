@@ -542,6 +542,21 @@ def gpu_figures(call, steps, warmup, samples):
     return statistics.median(single), single, back
 
 
+def vendor_gemm_tflops(dev, n=8192, steps=10):
+    """Same-box reference for the MFMA roofline: TFLOP/s of a library bf16 GEMM
+    (torch.matmul, hipBLASLt) on N(0,1) inputs, back to back. The matrix cores'
+    switching activity sets the power-limited clock, so random data reach less
+    than the nominal dense peak even in the vendor GEMM."""
+    import torch
+    gen = torch.Generator(device=dev).manual_seed(7)
+    a = torch.randn(n, n, device=dev, generator=gen).to(torch.bfloat16)
+    b = torch.randn(n, n, device=dev, generator=gen).to(torch.bfloat16)
+    ms = region_ms(lambda: torch.matmul(a, b), steps, 3)
+    del a, b
+    torch.cuda.empty_cache()
+    return 2 * n ** 3 / (ms / steps * 1e-3) / 1e12
+
+
 def prefill_record(kern, inputs, flops, qkv_bytes, steps, warmup, samples):
     """Figures of one direct prefill workload; the timed single calls are the step."""
     med, single, back = gpu_figures(lambda: kern(*inputs), steps, warmup, samples)
@@ -624,6 +639,11 @@ def main():
                           args.steps, args.warmup, args.steps)
     head["roofline"]["traffic"] = traffic_from_profile("prefill_direct")
     head["roofline"]["traffic_source"] = str(TRAFFIC_SUMMARY.relative_to(ROOT))
+    gemm = vendor_gemm_tflops(dev)
+    head["roofline"]["vendor_gemm_tflops"] = gemm
+    head["roofline"]["frac_of_vendor_gemm"] = head["roofline"]["achieved"] / gemm
+    head["roofline"]["vendor_gemm"] = ("torch.matmul bf16 8192^3 (hipBLASLt), N(0,1) inputs, "
+                                       "back to back on the same box")
 
     # ---- companion: Q32768 / KV2048 prefill ------------------------------
     big_sq = 32768
@@ -639,6 +659,7 @@ def main():
                          O.algorithmic_bytes([kv] * b, big_sq, h, d, kv // page),
                          big_steps, max(2, args.warmup // 5), big_steps)
     big["workload"] = "Q32768/KV2048 B2H8 D128 BF16 page128 non-causal full cache"
+    big["roofline"]["frac_of_vendor_gemm"] = big["roofline"]["achieved"] / gemm
     big["steps"] = big_steps
 
     # ---- decode: Q1 / KV32768 -------------------------------------------
