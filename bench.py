@@ -245,15 +245,19 @@ def suite_decode_scan(args, emit):
             for req in (None, 1, 4, 16):
                 if req is not None and req > kv // 32:
                     continue
+                # The automatic split with the host-known lengths, as mha_paged_decode
+                # plans it (cost model, length-balanced splits).
                 kern = build_kernel(4, sq, h, d, k.shape[0], kv // page, page, False,
                                     "bfloat16" if name == "bf16" else "float16", 0,
-                                    num_splits=req)
+                                    num_splits=req,
+                                    cache_lengths=tuple(lengths.tolist()) if req is None else None)
                 _checked(kern, dinputs, expected, dtype, f"imbalanced {name} q{sq} splits={req}")
                 single, back = _time_call(lambda: kern(*dinputs), args.scan_samples,
                                           args.scan_warmup)
                 emit({"suite": "decode-imbalanced", "dtype": name, "batch": 4, "heads": h,
                       "head_dim": d, "q_len": sq, "kv_len": kv, "lengths": lengths.tolist(),
                       "requested_splits": req, "num_splits": kern.num_splits,
+                      "split_keys": kern.split_keys,
                       "grid": kern.compute_grid, "us_per_call": single, "us_back_to_back": back,
                       "hbm_gbs": nbytes / (single * 1e-6) / 1e9})
 

@@ -10,7 +10,7 @@ import pathlib
 import threading
 
 LIBRARY = pathlib.Path(__file__).resolve().with_name("libfgw_mha.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 FGW_MHA_OK, FGW_MHA_EINVAL, FGW_MHA_EUNSUPPORTED, FGW_MHA_EHIP = 0, -1, -2, -3
 NOALLOC_SCRATCH_BYTES = 32 << 20  # FGW_MHA_NOALLOC_SCRATCH_BYTES
@@ -28,7 +28,8 @@ class Shape(ctypes.Structure):
 
 
 class Request(ctypes.Structure):
-    _fields_ = [("num_splits", c_int32), ("persistent_programs", c_int32), ("layout", c_int32)]
+    _fields_ = [("num_splits", c_int32), ("persistent_programs", c_int32), ("layout", c_int32),
+                ("split_keys", c_int32)]
 
 
 class DeviceInfo(ctypes.Structure):
@@ -40,7 +41,7 @@ class Plan(ctypes.Structure):
                 ("num_splits", c_int32), ("query_tile_tasks", c_int32),
                 ("work_items", c_int32), ("grid", c_int32), ("threads", c_int32),
                 ("execution_mode", c_int32), ("dim_padded", c_int32),
-                ("parts_floats", c_int64), ("lse_floats", c_int64)]
+                ("parts_floats", c_int64), ("lse_floats", c_int64), ("split_keys", c_int32)]
 
 
 class Tensors(ctypes.Structure):

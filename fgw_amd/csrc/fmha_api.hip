@@ -107,6 +107,7 @@ int hip_fail(hipError_t e, const char* what) {
 }
 
 constexpr int kMaxSplits = 128;
+static_assert(kMaxBalancedBatch == FGW_MHA_MAX_BALANCED_BATCH, "balanced-split batch cap");
 constexpr int kAutoMaxSplits = 64;
 constexpr int kMinRoundsPerSplit = 2;
 
@@ -216,7 +217,10 @@ int check_plan(const fgw_mha_shape* s, const fgw_mha_plan_t* p) {
   if (p->rows_per_tile != rows || p->q_tiles != q_tiles || p->query_tile_tasks != tasks ||
       p->num_splits < 1 || p->num_splits > kMaxSplits ||
       p->work_items != tasks * p->num_splits || p->grid < 1 || p->grid > p->work_items ||
-      p->dim_padded != dim_tile(s->dim) || p->execution_mode != (p->num_splits > 1 ? 1 : 0))
+      p->dim_padded != dim_tile(s->dim) || p->execution_mode != (p->num_splits > 1 ? 1 : 0) ||
+      p->split_keys < 0 ||
+      (p->split_keys > 0 && (p->layout != kLayoutKey || p->num_splits < 2 ||
+                             s->batch > kMaxBalancedBatch)))
     return fail(FGW_MHA_EINVAL, "plan does not match the shape; call fgw_mha_plan");
   return FGW_MHA_OK;
 }
@@ -259,6 +263,7 @@ FwdParams make_params(const fgw_mha_shape* s, const fgw_mha_plan_t* p, const fgw
   f.q_tiles = p->q_tiles;
   f.work = p->work_items;
   f.mode = mode;
+  f.split_keys = mode == 1 ? p->split_keys : 0;
   page_divisor((uint32_t)s->page_size, &f.page_magic, &f.page_shift);
   f.scale_log2 = (float)(1.4426950408889634 / __builtin_sqrt((double)s->dim));
   f.segs = nullptr;
@@ -307,6 +312,9 @@ int launch_merge_kernel(const fgw_mha_shape* s, const fgw_mha_plan_t* p, const f
   m.heads = s->heads;
   m.dim = s->dim;
   m.splits = p->num_splits;
+  m.lengths = t->cache_seqlens;
+  m.split_keys = p->split_keys;
+  m.capacity = s->width * s->page_size;
   const hipError_t err = launch_merge(s->dtype == FGW_MHA_BFLOAT16, m, stream);
   return err == hipSuccess ? FGW_MHA_OK : hip_fail(err, "merge kernel launch");
 }
@@ -382,6 +390,11 @@ int fgw_mha_plan(const fgw_mha_shape* s, const fgw_mha_request* req,
   }
   const int64_t work = tasks * splits;
   if (work > INT32_MAX) return fail(FGW_MHA_EUNSUPPORTED, "work items exceed 2^31");
+  if (req->split_keys < 0) return fail(FGW_MHA_EINVAL, "split_keys must be 0 or positive");
+  if (req->split_keys > 0 && (layout != kLayoutKey || splits < 2 || s->batch > kMaxBalancedBatch))
+    return fail(FGW_MHA_EINVAL,
+                "split_keys (length-balanced splits) needs the key layout, num_splits >= 2 and "
+                "B <= %d", kMaxBalancedBatch);
 
   int64_t grid = work;
   if (req->persistent_programs < -1)
@@ -411,6 +424,7 @@ int fgw_mha_plan(const fgw_mha_shape* s, const fgw_mha_request* req,
   out->dim_padded = dpad;
   out->parts_floats = splits > 1 ? (int64_t)s->batch * s->heads * splits * s->sq * s->dim : 0;
   out->lse_floats = splits > 1 ? (int64_t)s->batch * s->heads * splits * s->sq : 0;
+  out->split_keys = req->split_keys;
   return FGW_MHA_OK;
 }
 
@@ -467,6 +481,8 @@ int fgw_mha_merge(const fgw_mha_shape* s, const fgw_mha_plan_t* p, const fgw_mha
   int rc = check_shape(s);
   if (!rc) rc = check_plan(s, p);
   if (!rc) rc = check_tensors(t, false, true, true);
+  if (!rc && p->split_keys > 0 && !t->cache_seqlens)
+    rc = fail(FGW_MHA_EINVAL, "a length-balanced plan merges by cache_seqlens; it is NULL");
   if (rc) return rc;
   return launch_merge_kernel(s, p, t, stream);
 }

@@ -57,17 +57,28 @@ __device__ __forceinline__ void merge_one(const float* ls, int64_t lse_stride, c
   *reinterpret_cast<u32x2*>(dst) = w;
 }
 
+// Splits row (b, ., .) of a merge reads: all slots, or the balanced count
+// of request b (balanced_splits over its clamped length).
+__device__ __forceinline__ int merge_splits(const MergeParams& p, int b) {
+  if (p.split_keys <= 0) return p.splits;
+  int len = p.lengths[b];
+  len = len < 0 ? 0 : (len > p.capacity ? p.capacity : len);
+  return balanced_splits(len, p.split_keys, p.splits);
+}
+
+// Rows [q0, q0 + rows) of (b, h): `slots` is the workspace's split dimension,
+// the first `used` slots are merged.
 template <bool BF16>
 __device__ __forceinline__ void merge_rows(const float* parts, const float* lse, void* out, int sq,
-                                           int heads, int dim, int splits, int b, int h, int q0,
-                                           int rows, int tid, int nthreads) {
+                                           int heads, int dim, int slots, int used, int b, int h,
+                                           int q0, int rows, int tid, int nthreads) {
   const int d4n = dim / 4;
-  const int64_t bhs = ((int64_t)b * heads + h) * splits;
+  const int64_t bhs = ((int64_t)b * heads + h) * slots;
   for (int idx = tid; idx < rows * d4n; idx += nthreads) {
     const int q = q0 + idx / d4n, d0 = 4 * (idx % d4n);
     u16* dst = static_cast<u16*>(out) + (((int64_t)b * sq + q) * heads + h) * dim + d0;
     merge_one<BF16>(lse + bhs * sq + q, sq, parts + (bhs * sq + q) * dim + d0,
-                    (int64_t)sq * dim, splits, dst);
+                    (int64_t)sq * dim, used, dst);
   }
 }
 
@@ -80,7 +91,8 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(MergeParams p, int
   const int bh = blockIdx.x / groups;
   const int q0 = g * rows_per_wg;
   const int rows = p.sq - q0 < rows_per_wg ? p.sq - q0 : rows_per_wg;
-  merge_rows<BF16>(p.parts, p.lse, p.out, p.sq, p.heads, p.dim, p.splits, bh / p.heads,
+  const int b = bh / p.heads;
+  merge_rows<BF16>(p.parts, p.lse, p.out, p.sq, p.heads, p.dim, p.splits, merge_splits(p, b), b,
                    bh % p.heads, q0, rows, threadIdx.x, kMergeThreads);
 }
 
@@ -110,22 +122,23 @@ __global__ __launch_bounds__(kMergeThreads) void merge_wide_kernel(MergeParams p
   const float* ls = p.lse + base;
   const float* ps = p.parts + base * p.dim + 4 * c;
   const int64_t part_stride = (int64_t)p.sq * p.dim;
+  const int used = merge_splits(p, b);
   float peak = kNegBig, tot = 0.0f;
   f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
   if (act) {
-    for (int s0 = g; s0 < p.splits; s0 += kMergeChunk * G) {
+    for (int s0 = g; s0 < used; s0 += kMergeChunk * G) {
       float x[kMergeChunk];
       f32x4 v[kMergeChunk];
 #pragma unroll
       for (int i = 0; i < kMergeChunk; ++i) {
-        const int s = s0 + i * G < p.splits ? s0 + i * G : g;  // clamped; weight 0 below
+        const int s = s0 + i * G < used ? s0 + i * G : g;  // clamped; weight 0 below
         x[i] = ls[(int64_t)s * p.sq];
         v[i] = *reinterpret_cast<const f32x4*>(ps + (int64_t)s * part_stride);
       }
       float cpeak = peak;
 #pragma unroll
       for (int i = 0; i < kMergeChunk; ++i) {
-        const bool live = s0 + i * G < p.splits && x[i] > -1.0e29f;
+        const bool live = s0 + i * G < used && x[i] > -1.0e29f;
         cpeak = live ? fmaxf(cpeak, x[i]) : cpeak;
       }
       const float keep = expf(peak - cpeak);
@@ -133,7 +146,7 @@ __global__ __launch_bounds__(kMergeThreads) void merge_wide_kernel(MergeParams p
       acc *= keep;
 #pragma unroll
       for (int i = 0; i < kMergeChunk; ++i) {
-        const bool live = s0 + i * G < p.splits && x[i] > -1.0e29f;
+        const bool live = s0 + i * G < used && x[i] > -1.0e29f;
         const float wgt = live ? expf(x[i] - cpeak) : 0.0f;
         tot += wgt;
         acc += live ? v[i] * wgt : f32x4{0.0f, 0.0f, 0.0f, 0.0f};

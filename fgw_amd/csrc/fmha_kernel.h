@@ -77,6 +77,9 @@ constexpr float kNegBig = -1.0e30f;  // running-max floor and empty-split LSE
 constexpr float kSoftmaxSumBound = 8192.0f;  // lane row-sum bound before O/l are rescaled
 constexpr int kNumXcd = 8;
 constexpr int kLdsBudget = 160 * 1024;
+// Largest batch of a length-balanced split plan (FwdParams::split_keys > 0):
+// the per-request split prefix sums live in LDS.
+constexpr int kMaxBalancedBatch = 1024;
 
 // Source of every masked 16-byte chunk: read-only zeros in device memory.
 static __device__ __attribute__((aligned(64))) const u32 kZeroChunk[16] = {0};
@@ -175,7 +178,11 @@ struct Cfg {
   static constexpr int OSTRIDE = DPAD + 4;  // combine buffer row stride (floats)
   static constexpr int COMB_BYTES =
       NWK > 1 ? (2 * NWK * ROWS_WAVE + NWK * ROWS_WAVE * OSTRIDE) * 4 : 0;
-  static constexpr int LDS_BYTES = CMax<TILES_BYTES, COMB_BYTES>::value;
+  // Key layout: per-request split prefix sums of a length-balanced plan,
+  // after the tiles and the combine buffer.
+  static constexpr int PREFIX_OFF = CMax<TILES_BYTES, COMB_BYTES>::value;
+  static constexpr int PREFIX_BYTES = LAYOUT == kLayoutKey ? (kMaxBalancedBatch + 1) * 4 : 0;
+  static constexpr int LDS_BYTES = PREFIX_OFF + PREFIX_BYTES;
   // DMA: one wave instruction fills 1 KB (64 lanes x 16 bytes) of a tile.
   static constexpr int INSTR = TILE_BYTES / 1024;
   static constexpr int INSTR_PER_WAVE = INSTR / NWQ;
@@ -189,6 +196,9 @@ struct Cfg {
   static_assert((DPAD & (DPAD - 1)) == 0 && DPAD >= 32 && DPAD <= 256, "head dim tile");
   static_assert(TILE_BYTES % 1024 == 0 && INSTR % NWQ == 0 && 64 % CPR == 0, "DMA granularity");
   static_assert(LDS_BYTES <= kLdsBudget, "LDS budget of one CU");
+  static_assert(LAYOUT != kLayoutKey || (THREADS * 4 >= kMaxBalancedBatch &&
+                                         THREADS * 4 <= TILES_BYTES),
+                "balanced-split prefix scan: 4 requests per thread, scratch in the tiles");
 };
 
 // LDS DMA (global_load_lds_dwordx4) for kernels that place their own waits
@@ -563,6 +573,56 @@ __device__ __forceinline__ int split_bound(int nblk, int s, int splits) {
   return (int)((int64_t)nblk * s / splits);
 }
 
+// Splits of a request of len live keys in a length-balanced plan: enough
+// that none holds more than split_keys keys, at least 1, at most splits.
+__device__ __forceinline__ int balanced_splits(int len, int split_keys, int splits) {
+  const int s = len > 0 ? (len - 1) / split_keys + 1 : 1;
+  return s < splits ? s : splits;
+}
+
+// Exclusive prefix sums of the balanced split counts over the batch, into
+// pre[0 .. B] (pre[B] = total), by every thread of the workgroup; tmp holds
+// THREADS ints of scratch. Each thread takes up to 4 consecutive requests;
+// the per-thread sums are scanned in LDS (Hillis-Steele). Ends with a barrier.
+template <class C>
+__device__ void balanced_prefix(const FwdParams& p, const int32_t* lengths, int capacity,
+                                int32_t* pre, int32_t* tmp, int tid) {
+  const int per = (p.batch + C::THREADS - 1) / C::THREADS;  // <= 4
+  const int b0 = tid * per;
+  int cnt[4];
+  int local = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int b = b0 + i;
+    int c = 0;
+    if (i < per && b < p.batch) {
+      int len = lengths[b];
+      len = len < 0 ? 0 : (len > capacity ? capacity : len);
+      c = balanced_splits(len, p.split_keys, p.splits);
+    }
+    cnt[i] = c;
+    local += c;
+  }
+  tmp[tid] = local;
+  __syncthreads();
+  for (int off = 1; off < C::THREADS; off <<= 1) {
+    const int add = tid >= off ? tmp[tid - off] : 0;
+    __syncthreads();
+    tmp[tid] += add;
+    __syncthreads();
+  }
+  int run = tmp[tid] - local;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (i < per && b0 + i < p.batch) {
+      pre[b0 + i] = run;
+      run += cnt[i];
+    }
+  }
+  if (tid == C::THREADS - 1) pre[p.batch] = tmp[tid];
+  __syncthreads();
+}
+
 // Page id of the page holding logical position pos.
 __device__ __forceinline__ int32_t page_id(const FwdParams& p, const int32_t* table_b, int pos) {
   return table_b[div_page((u32)pos, p.page_magic, p.page_shift)];
@@ -589,20 +649,33 @@ __global__ __launch_bounds__(C::THREADS) void fwd_kernel(FwdParams p,
 
   const int grid = gridDim.x;
   const int prog = xcd_remap(blockIdx.x, grid);
+  const int capacity = p.width * p.page_size;
+  const int tasks = p.batch * p.heads * p.q_tiles;
+  // Length-balanced splits (key layout, partial mode): request b takes
+  // pre[b + 1] - pre[b] splits; its work items are [pre[b], pre[b + 1]) x
+  // H x q_tiles, split-major (see the decode of w below).
+  const bool balanced = C::LAYOUT == kLayoutKey && p.mode == 1 && p.split_keys > 0;
+  const int32_t* const pre = reinterpret_cast<const int32_t*>(smem + C::PREFIX_OFF);
+  int work = p.work;
+  if constexpr (C::LAYOUT == kLayoutKey) {
+    if (balanced) {
+      balanced_prefix<C>(p, lengths, capacity, reinterpret_cast<int32_t*>(smem + C::PREFIX_OFF),
+                         reinterpret_cast<int32_t*>(smem), tid);
+      work = __builtin_amdgcn_readfirstlane(pre[p.batch]) * p.heads * p.q_tiles;
+    }
+  }
   int first, count;
   if (p.mode == 2) {  // static schedule: this program's segments
     first = p.seg_offsets[prog];
     count = p.seg_offsets[prog + 1] - first;
   } else {  // contiguous range of work items
-    const int per = p.work / grid, rem = p.work % grid;
+    const int per = work / grid, rem = work % grid;
     first = prog * per + (prog < rem ? prog : rem);
     count = per + (prog < rem ? 1 : 0);
   }
-  const int capacity = p.width * p.page_size;
-  const int tasks = p.batch * p.heads * p.q_tiles;
 
   for (int it = 0; it < count; ++it) {
-    int w = first + it, split = 0, slot = -1, seg_lo = 0, seg_hi = 0;
+    int w = first + it, split = 0, slot = -1, seg_lo = 0, seg_hi = 0, nsplit = p.splits;
     if (p.mode == 2) {
       const int32_t* sg = p.segs + 4 * (int64_t)w;
       w = sg[0];
@@ -611,6 +684,21 @@ __global__ __launch_bounds__(C::THREADS) void fwd_kernel(FwdParams p,
       slot = sg[3];
       // Segments a host plan cannot produce are skipped whole (uniform).
       if (w < 0 || w >= tasks || slot >= p.slots || sg[1] < 0 || sg[2] < 0) continue;
+    } else if (balanced) {
+      // g = w / (H q_tiles) = pre[b] + split for the request b with
+      // pre[b] <= g < pre[b + 1] (pre is strictly increasing: every request
+      // has at least one split); the rest of w is (h, q tile).
+      const int hq = p.heads * p.q_tiles;
+      const int g = w / hq;
+      int lo = 0, hi = p.batch;
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (__builtin_amdgcn_readfirstlane(pre[mid]) <= g) lo = mid; else hi = mid;
+      }
+      const int pb = __builtin_amdgcn_readfirstlane(pre[lo]);
+      split = g - pb;
+      nsplit = __builtin_amdgcn_readfirstlane(pre[lo + 1]) - pb;
+      w = lo * hq + w % hq;
     } else {
       split = w % p.splits;
       w /= p.splits;
@@ -631,7 +719,7 @@ __global__ __launch_bounds__(C::THREADS) void fwd_kernel(FwdParams p,
     constexpr int kStep = C::NWK * C::BN;
     int spec_pos = -1;
     int32_t spec0 = 0, spec1 = 0;
-    if (p.mode != 2 && !p.causal) {
+    if (p.mode != 2 && !p.causal && !balanced) {
       const int nfull = (capacity + C::BN - 1) / C::BN;
       spec_pos = (split_bound(nfull, split, p.splits) + wk) * C::BN;
       if (spec_pos < capacity) spec0 = page_id(p, table_b, spec_pos);
@@ -649,8 +737,8 @@ __global__ __launch_bounds__(C::THREADS) void fwd_kernel(FwdParams p,
       blk_end = seg_hi < nblk ? seg_hi : nblk;
       blk_begin = seg_lo < blk_end ? seg_lo : blk_end;
     } else {
-      blk_begin = split_bound(nblk, split, p.splits);
-      blk_end = split_bound(nblk, split + 1, p.splits);
+      blk_begin = split_bound(nblk, split, nsplit);
+      blk_end = split_bound(nblk, split + 1, nsplit);
     }
     const int cnt = blk_end - blk_begin;
     const int my_n = cnt > wk ? (cnt - wk + C::NWK - 1) / C::NWK : 0;

@@ -41,6 +41,9 @@ struct FwdParams {
   const int32_t* seg_offsets;
   int32_t slots;
   int32_t seg_scale;  // kernel key blocks per schedule key block
+  // Length-balanced splits (key layout, mode 1): request b takes
+  // balanced_splits(len_b, split_keys, splits) splits; 0 = even splits.
+  int32_t split_keys;
 };
 
 struct MergeParams {
@@ -48,6 +51,10 @@ struct MergeParams {
   const float* lse;       // [B, H, S, Sq]
   void* out;              // [B, Sq, H, D]
   int32_t batch, sq, heads, dim, splits;
+  // Length-balanced splits: row (b, ., .) merges the first
+  // balanced_splits(len_b, split_keys, splits) slots; 0 = all slots.
+  const int32_t* lengths;  // [B], read only when split_keys > 0
+  int32_t split_keys, capacity;
 };
 
 // Merge of the static schedule's split tiles: group g = (task, first slot,

@@ -114,6 +114,10 @@ class _Launch(_launch.Launcher):
         self.requested_split_policy = meta["requested_split_policy"]
         self.split_policy = meta["split_policy"]
         self.num_splits = plan.num_splits
+        # Length-balanced splits: request b takes clamp(ceil(len_b / split_keys),
+        # 1, num_splits) of the num_splits slots; 0 = every request num_splits.
+        self.split_keys = plan.split_keys
+        self.split_balance = "length" if plan.split_keys else "even"
         self.query_tile_tasks = plan.query_tile_tasks
         self.execution_mode = "split_and_merge" if plan.execution_mode else "direct_single_split"
         self.execution_path = ROUTE
@@ -176,16 +180,26 @@ class _Launch(_launch.Launcher):
         return (parts.view(s.batch, s.heads, self.num_splits, s.sq, s.dim),
                 lse.view(s.batch, s.heads, self.num_splits, s.sq))
 
-    def _merge(self, parts, lse):
+    def _merge(self, parts, lse, cache_seqlens=None):
+        """Output from the partials. A length-balanced plan (split_keys > 0)
+        merges request b's first clamp(ceil(len_b / split_keys), 1, S) slots
+        and needs the call's cache_seqlens."""
         s = self._shape
         if (parts.dtype != torch.float32 or lse.dtype != torch.float32
                 or parts.numel() != self._plan.parts_floats or lse.numel() != self._plan.lse_floats
                 or not parts.is_contiguous() or not lse.is_contiguous()
                 or parts.device != self._device or lse.device != self._device):
             raise ValueError("merge expects this kernel's contiguous fp32 partials and LSE")
+        if cache_seqlens is not None and (cache_seqlens.dtype != torch.int32
+                                          or tuple(cache_seqlens.shape) != self._meta_shapes[1]
+                                          or cache_seqlens.device != self._device):
+            raise ValueError("cache_seqlens must be this kernel's int32 [B] lengths on its GPU")
+        if self.split_keys and cache_seqlens is None:
+            raise ValueError("a length-balanced plan merges by cache_seqlens")
         out = torch.empty(self._out_shape, dtype=self._dtype, device=self._device)
-        t = _lib.Tensors(None, None, None, None, None, out.data_ptr(), parts.data_ptr(),
-                         lse.data_ptr())
+        t = _lib.Tensors(None, None, None, None,
+                         None if cache_seqlens is None else cache_seqlens.data_ptr(),
+                         out.data_ptr(), parts.data_ptr(), lse.data_ptr())
         _lib.check(self._lib.fgw_mha_merge(ctypes.byref(s), ctypes.byref(self._plan),
                                            ctypes.byref(t), self._stream()))
         return out
@@ -193,7 +207,7 @@ class _Launch(_launch.Launcher):
 
 @lru_cache(maxsize=128)
 def _planned(batch, sq, heads, dim, pool_rows, width, page_size, causal, name, device_index,
-             splits, persistent, layout, meta):
+             splits, persistent, layout, meta, split_keys=0):
     """Launch callable of one (static shape, split request, grid request,
     layout): the unit the plan depends on. Ragged lengths reach the cost model
     before this cache, so a decode step with new lengths re-plans nothing
@@ -201,7 +215,7 @@ def _planned(batch, sq, heads, dim, pool_rows, width, page_size, causal, name, d
     device = _device_info(device_index)
     shape = _lib.Shape(batch, sq, heads, dim, pool_rows, width, page_size, int(bool(causal)),
                        _lib.DTYPE_BFLOAT16 if name == "bfloat16" else _lib.DTYPE_FLOAT16)
-    plan = _lib.plan(shape, _lib.Request(splits, persistent, _LAYOUTS[layout]), device)
+    plan = _lib.plan(shape, _lib.Request(splits, persistent, _LAYOUTS[layout], split_keys), device)
     return _Launch(shape, plan, device_index, _DTYPES[name], dict(meta))
 
 
@@ -243,6 +257,7 @@ def build_kernel(batch, sq, heads, dim, pool_rows, width, page_size, causal, dty
     if layout not in _LAYOUTS:
         raise ValueError("layout must be None, 'query', 'key' or 'prefill'")
 
+    split_keys = 0
     if num_splits is not None:
         splits, policy = num_splits, "explicit"
     else:
@@ -261,13 +276,19 @@ def build_kernel(batch, sq, heads, dim, pool_rows, width, page_size, causal, dty
                 lengths = (width * page_size,) * batch
             splits = split_cost_model.select_splits(batch, sq, heads, dim, width * page_size,
                                                     tuple(lengths), _device_info(device_index))
+            if cache_lengths is not None and layout is None and sq <= 32:
+                # Ragged lengths: the same number of work items, balanced by length.
+                balanced = split_cost_model.balanced_split_keys(tuple(lengths), splits,
+                                                                width * page_size)
+                if balanced is not None:
+                    splits, split_keys = balanced
         else:
             splits = 0
         policy = split_policy
     meta = (("persistent_programs", persistent_programs),
             ("requested_split_policy", requested_split_policy), ("split_policy", policy))
     return _planned(batch, sq, heads, dim, pool_rows, width, page_size, bool(causal), name,
-                    device_index, splits, persistent, layout, meta)
+                    device_index, splits, persistent, layout, meta, split_keys)
 
 
 def mha_paged_decode(q, k_cache, v_cache, block_table, cache_seqlens, page_size, is_causal=False,

@@ -106,6 +106,44 @@ def predict(batch, sq, heads, dim, lengths, splits, num_cus, wg_per_cu, model) -
     return sum(w * v for w, v in zip(model["weights"], x))
 
 
+MAX_BALANCED_BATCH = 1024  # FGW_MHA_MAX_BALANCED_BATCH
+# split_keys values of balanced plans: 32 * 2^(j / 16), rounded up (steps of
+# 4.4%), so that a decode step whose lengths grew by a few tokens usually
+# reuses its plan. 32 .. 2^30.
+_KEY_GRID = tuple(sorted({math.ceil(32 * 2 ** (j / 16)) for j in range(0, 16 * 25 + 1)}))
+
+
+def balanced_split_keys(lengths, splits, capacity_tokens):
+    """(workspace splits, split_keys) of a length-balanced plan with the work
+    items of `splits` even splits per request, or None where it would not
+    shorten the longest work item (uniform lengths, one split, large batch).
+
+    Request b then takes clamp(ceil(len_b / split_keys), 1, workspace splits)
+    splits. split_keys is the smallest value of _KEY_GRID with
+    sum_b max(1, ceil(len_b / split_keys)) <= B * splits; the workspace split
+    count is the next power of two of the largest request's count, at most
+    128 and at most the table's 32-token tiles (the planner's limits).
+    """
+    batch = len(lengths)
+    if splits < 2 or batch < 2 or batch > MAX_BALANCED_BATCH or len(set(lengths)) < 2:
+        return None
+    longest = max(lengths)
+    if longest <= 0:
+        return None
+    budget = batch * splits
+    items = lambda k: sum(max(1, -(-n // k)) for n in lengths)  # noqa: E731
+    keys = next((k for k in _KEY_GRID if items(k) <= budget), None)
+    if keys is None or keys >= -(-longest // splits):
+        return None  # no shorter longest item than the even split's
+    cap = min(128, max(1, -(-capacity_tokens // 32)))
+    need = -(-longest // keys)
+    slots = 1
+    while slots < need:
+        slots *= 2
+    slots = min(slots, cap)
+    return (slots, keys) if slots >= 2 else None
+
+
 def select_splits(batch, sq, heads, dim, capacity_tokens, lengths, device, model=None) -> int:
     """Split count with the lowest predicted latency (ties -> fewer splits)."""
     model = model or load_model()

@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define FGW_MHA_ABI_VERSION 3
+#define FGW_MHA_ABI_VERSION 4
 
 typedef enum {
   FGW_MHA_OK = 0,
@@ -79,7 +79,16 @@ typedef struct {
   int32_t num_splits;          /* 0 = automatic; else 1,2,4,...,128 */
   int32_t persistent_programs; /* -1 = CU-derived cap (uncapped for causal), 0 = uncapped grid, n > 0 = cap */
   int32_t layout;              /* fgw_mha_layout */
+  int32_t split_keys;          /* 0 = every request's keys split evenly into num_splits; > 0 =
+                                  splits balanced by length (key layout, num_splits > 1, B <=
+                                  FGW_MHA_MAX_BALANCED_BATCH): request b takes
+                                  clamp(ceil(len_b / split_keys), 1, num_splits) splits, so
+                                  ragged requests get work items of similar size. No reference
+                                  counterpart (the reference splits every request evenly). */
 } fgw_mha_request;
+
+/* Largest batch of a length-balanced split plan (split_keys > 0). */
+#define FGW_MHA_MAX_BALANCED_BATCH 1024
 
 /* Device facts the planner needs; filled by fgw_mha_query_device. */
 typedef struct {
@@ -103,6 +112,9 @@ typedef struct {
   int32_t dim_padded;      /* head-dim tile of the selected kernel */
   int64_t parts_floats;    /* fp32 elements of the partial-output workspace (0 if direct) */
   int64_t lse_floats;      /* fp32 elements of the LSE workspace (0 if direct) */
+  int32_t split_keys;      /* request.split_keys of a split plan (0: even splits); work_items and
+                              the workspaces are then upper bounds, slot s of request b is used
+                              for s < clamp(ceil(len_b / split_keys), 1, num_splits) */
 } fgw_mha_plan_t;
 
 /* Device buffers of one call. Workspaces are owned by the caller and sized

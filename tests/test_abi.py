@@ -98,6 +98,25 @@ def test_plan_split_rules(lib):
         _lib.plan(shape(kv=128), _lib.Request(8, -1, -1), DEVICE)
 
 
+def test_plan_length_balanced_splits(lib):
+    """split_keys > 0: accepted for the key layout with >= 2 splits and B <= 1024,
+    carried into the plan; rejected otherwise."""
+    key = _lib.plan(shape(sq=1, kv=8192), _lib.Request(16, -1, _lib.LAYOUT_KEY, 600), DEVICE)
+    assert (key.layout, key.num_splits, key.split_keys) == (_lib.LAYOUT_KEY, 16, 600)
+    even = _lib.plan(shape(sq=1, kv=8192), _lib.Request(16, -1, _lib.LAYOUT_KEY), DEVICE)
+    assert even.split_keys == 0 and even.work_items == key.work_items
+    for req, s in ((_lib.Request(16, -1, _lib.LAYOUT_QUERY, 600), shape(sq=1, kv=8192)),
+                   (_lib.Request(1, -1, _lib.LAYOUT_KEY, 600), shape(sq=1, kv=8192)),
+                   (_lib.Request(16, -1, _lib.LAYOUT_KEY, -1), shape(sq=1, kv=8192))):
+        with pytest.raises(ValueError, match="split_keys"):
+            _lib.plan(s, req, DEVICE)
+    big = shape(sq=1, kv=8192)
+    big.batch = 1025
+    big.pool_rows = 1025 * 8192
+    with pytest.raises(ValueError, match="split_keys"):
+        _lib.plan(big, _lib.Request(16, -1, _lib.LAYOUT_KEY, 600), DEVICE)
+
+
 @pytest.mark.parametrize("field,value,message", [
     ("dim", 24, "divisible by 16"),
     ("dim", 272, "D must be"),

@@ -207,6 +207,54 @@ def test_wide_merge_many_splits():
                                    rtol=8e-3, atol=1e-5, msg=label)
 
 
+def test_length_balanced_splits():
+    """Ragged decode batches under the automatic split take length-balanced
+    splits (request b: clamp(ceil(len_b / split_keys), 1, S) slots). Outputs
+    against the oracle with NaN in every unread pool row; the partial and merge
+    components (the merge given the lengths) equal the fused call bit for bit;
+    with uniform lengths a balanced plan equals the even plan bit for bit."""
+    from fgw_amd.operators.mha.current import build_kernel, mha_paged_decode
+    cases = (("imbalanced_kv32768", 4, 1, 8, 128, 128, 256, [13321, 16319, 6592, 12115],
+              torch.bfloat16),
+             ("imbalanced_q16", 4, 16, 8, 128, 128, 64, [4635, 4285, 4326, 1917], torch.float16),
+             ("empty_and_short", 5, 1, 2, 128, 64, 64, [0, 4096, 17, 1000, 2500], torch.bfloat16),
+             ("page32_q7", 3, 7, 4, 128, 32, 64, [2048, 100, 1500], torch.bfloat16))
+    for (name, b, sq, h, d, page, width, lens, dtype) in cases:
+        case = (name, b, sq, h, d, page, width)
+        q, k, v, table = O.make_inputs(case, 5, dtype)
+        lengths = torch.tensor(lens, dtype=torch.int32)
+        k, v = O.poison_unread(k, v, table, lengths, page)
+        dev = [x.cuda() for x in (q, k, v, table, lengths)]
+        got = mha_paged_decode(*dev, page_size=page)
+        torch.cuda.synchronize()
+        expected = O.reference(q, k, v, table, lengths, page, False)
+        check_output(got, expected, q, lengths, False, f"balanced {name}")
+        dname = "bfloat16" if dtype == torch.bfloat16 else "float16"
+        kern = build_kernel(b, sq, h, d, k.shape[0], width, page, False, dname, 0,
+                            cache_lengths=tuple(lens))
+        assert kern.split_balance == "length" and kern.split_keys > 0, (name, kern.num_splits)
+        fused = kern(*dev)
+        parts, lse = kern.partial_kernel(*dev)
+        merged = kern.merge_kernel(parts, lse, dev[4])
+        torch.cuda.synchronize()
+        assert torch.equal(fused, got) and torch.equal(merged, fused), name
+        with pytest.raises(ValueError, match="length-balanced"):
+            kern.merge_kernel(parts, lse)
+        log(f"{name}: splits {kern.num_splits} split_keys {kern.split_keys}")
+    # Uniform lengths: every request takes all slots, the even partition.
+    from fgw_amd import _lib
+    from fgw_amd.operators.mha.kernels import mha_paged_decode_hip as HIP
+    q, k, v, table, lengths = O.bench_inputs(2, 1, 8, 128, 128, 8192, torch.bfloat16)
+    dev = [x.cuda() for x in (q, k, v, table, lengths)]
+    even = build_kernel(2, 1, 8, 128, k.shape[0], 64, 128, False, "bfloat16", 0, num_splits=16)
+    meta = (("persistent_programs", HIP.PERSISTENT_DEVICE), ("requested_split_policy", "auto"),
+            ("split_policy", "explicit"))
+    balanced = HIP._planned(2, 1, 8, 128, k.shape[0], 64, 128, False, "bfloat16", 0, 16, -1,
+                            None, meta, 512)
+    assert balanced.split_keys == 512 and even.split_keys == 0
+    assert torch.equal(balanced(*dev), even(*dev))
+
+
 def test_headline_shapes():
     from fgw_amd.operators.mha.current import build_kernel
     for (b, sq, h, d, p, kv) in ((1, 1, 1, 128, 128, 512), (2, 4096, 8, 128, 128, 2048),

@@ -95,3 +95,22 @@ def test_calibration_file_is_scan_records():
     recs = [json.loads(x) for x in CALIBRATION.read_text().splitlines()]
     assert recs[0]["suite"] == "device" and recs[0]["num_cus"] == 256
     assert {r["suite"] for r in recs[1:]} >= {"decode-scan", "grid", "decode-imbalanced"}
+
+
+def test_balanced_split_keys():
+    # Config 4's imbalanced B4 lengths at KV 32768 with 8 even splits: the same
+    # 32 work items per head, none above 1650 keys (even: 16319 / 8 = 2040).
+    lens = (13321, 16319, 6592, 12115)
+    slots, keys = M.balanced_split_keys(lens, 8, 32768)
+    assert (slots, keys) == (16, 1650)
+    assert sum(-(-n // keys) for n in lens) <= 4 * 8 and -(-max(lens) // keys) <= slots
+    assert keys in M._KEY_GRID and max(M._KEY_GRID) <= 2 ** 30
+    # Nothing to balance: uniform lengths, one split, one request, too large a batch.
+    assert M.balanced_split_keys((8192, 8192), 16, 8192) is None
+    assert M.balanced_split_keys(lens, 1, 32768) is None
+    assert M.balanced_split_keys((5000,), 8, 8192) is None
+    assert M.balanced_split_keys(tuple(range(1, 1026)), 4, 2048) is None
+    # Empty requests still count one (empty) work item; slots stay within the table's tiles.
+    slots, keys = M.balanced_split_keys((0, 4096, 17, 1000, 2500), 4, 4096)
+    assert sum(max(1, -(-n // keys)) for n in (0, 4096, 17, 1000, 2500)) <= 5 * 4
+    assert 2 <= slots <= 128
