@@ -221,7 +221,8 @@ def _planned(batch, sq, heads, dim, pool_rows, width, page_size, causal, name, d
 
 def build_kernel(batch, sq, heads, dim, pool_rows, width, page_size, causal, dtype,
                  device_index=None, num_splits=None, split_policy="auto", full_kv_cache=False,
-                 persistent_programs=PERSISTENT_DEVICE, cache_lengths=None, layout=None):
+                 persistent_programs=PERSISTENT_DEVICE, cache_lengths=None, layout=None,
+                 split_keys=None):
     """Plan one static specialisation and return its launch callable.
 
     Arguments follow the reference build_kernel (v7.py:32-47) plus
@@ -233,7 +234,10 @@ def build_kernel(batch, sq, heads, dim, pool_rows, width, page_size, causal, dty
     alternate matrix and softmax phases, D in (32, 128]; "key" = waves split
     key blocks; None: key for Sq <= 32; prefill when its 256-row tiles fill
     the device, or, with KV splits, from Sq 1024, for D in (32, 128]; else
-    query). The reference caches build_kernel on its static arguments
+    query), and split_keys (extra; with an explicit num_splits >= 2 and the
+    key layout: request b takes clamp(ceil(len_b / split_keys), 1, num_splits)
+    splits; the automatic split chooses it itself for ragged host-known
+    lengths). The reference caches build_kernel on its static arguments
     (lru_cache(128), v7.py:32); here the split count is chosen first (the
     cost model reads cache_lengths only under the auto/cost_model policy)
     and the plans are cached per (shape, split count, grid, layout).
@@ -257,8 +261,11 @@ def build_kernel(batch, sq, heads, dim, pool_rows, width, page_size, causal, dty
     if layout not in _LAYOUTS:
         raise ValueError("layout must be None, 'query', 'key' or 'prefill'")
 
-    split_keys = 0
+    if split_keys is not None and (type(split_keys) is not int or split_keys < 1
+                                   or num_splits is None or num_splits < 2):
+        raise ValueError("split_keys needs a positive int and an explicit num_splits >= 2")
     if num_splits is not None:
+        split_keys = split_keys or 0
         splits, policy = num_splits, "explicit"
     else:
         if split_policy == "auto":
@@ -268,6 +275,7 @@ def build_kernel(batch, sq, heads, dim, pool_rows, width, page_size, causal, dty
                 full_kv_cache=full_kv_cache, num_cus=device.num_cus,
                 lengths_known=cache_lengths is not None, wg_per_cu=tuple(device.wg_per_cu))
             split_policy = "cost_model" if use_model else "legacy"
+        split_keys = 0
         if split_policy == "cost_model":
             lengths = cache_lengths
             if lengths is None:
