@@ -88,3 +88,34 @@ def test_graph_replays_of_the_static_fused_path():
     expected = O.chunked_reference(dq.cpu(), *host[1:], 128, False)
     rtol, atol = O.TOLERANCES[torch.bfloat16]
     torch.testing.assert_close(out.cpu(), expected, rtol=rtol, atol=atol)
+
+
+def test_graph_replays_of_a_balanced_plan_with_new_lengths():
+    """A length-balanced decode plan reads the lengths on the device (split
+    counts, work items, merge): one captured graph replays correctly after
+    the lengths are rewritten in place, bit for bit against the eager call,
+    and against the oracle for the last lengths."""
+    from fgw_amd.operators.mha.current import build_kernel
+    b, sq, h, d, page, kv = 4, 1, 8, 128, 128, 8192
+    width = kv // page
+    case = ("balanced_graph", b, sq, h, d, page, width)
+    q, k, v, table = O.make_inputs(case, 6, torch.bfloat16)
+    first = [4635, 4285, 4326, 1917]
+    kern = build_kernel(b, sq, h, d, k.shape[0], width, page, False, "bfloat16", 0,
+                        cache_lengths=tuple(first))
+    assert kern.split_balance == "length"
+    dq, dk, dv, dt = (x.cuda() for x in (q, k, v, table))
+    dl = torch.tensor(first, dtype=torch.int32, device="cuda")
+    call = lambda: kern(dq, dk, dv, dt, dl)  # noqa: E731
+    graph, out = _capture(call)
+    for lens in ([4635, 4285, 4326, 1917], [8192, 0, 100, 5000], [1, 8192, 8192, 3000]):
+        dl.copy_(torch.tensor(lens, dtype=torch.int32))
+        eager = call()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"graph replay differs from the eager call at {lens}"
+    lengths = torch.tensor(lens, dtype=torch.int32)
+    expected = O.reference(q, k, v, table, lengths, page, False)
+    rtol, atol = O.TOLERANCES[torch.bfloat16]
+    torch.testing.assert_close(out.cpu(), expected, rtol=rtol, atol=atol)
