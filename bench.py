@@ -658,7 +658,7 @@ def main():
     bflops = O.useful_flops([kv] * b, big_sq, h, d, False)
     bgot = bkern(*binputs)
     torch.cuda.synchronize()
-    big_steps = max(5, args.steps // 5)
+    big_steps = max(10, args.steps // 3)
     big = prefill_record(bkern, binputs, bflops,
                          O.algorithmic_bytes([kv] * b, big_sq, h, d, kv // page),
                          big_steps, max(2, args.warmup // 5), big_steps)
