@@ -196,9 +196,7 @@ struct Cfg {
   static_assert((DPAD & (DPAD - 1)) == 0 && DPAD >= 32 && DPAD <= 256, "head dim tile");
   static_assert(TILE_BYTES % 1024 == 0 && INSTR % NWQ == 0 && 64 % CPR == 0, "DMA granularity");
   static_assert(LDS_BYTES <= kLdsBudget, "LDS budget of one CU");
-  static_assert(LAYOUT != kLayoutKey || (THREADS * 4 >= kMaxBalancedBatch &&
-                                         THREADS * 4 <= TILES_BYTES),
-                "balanced-split prefix scan: 4 requests per thread, scratch in the tiles");
+  static_assert(kMaxBalancedBatch % 64 == 0, "balanced-split prefix scan: whole lanes");
 };
 
 // LDS DMA (global_load_lds_dwordx4) for kernels that place their own waits
@@ -581,45 +579,46 @@ __device__ __forceinline__ int balanced_splits(int len, int split_keys, int spli
 }
 
 // Exclusive prefix sums of the balanced split counts over the batch, into
-// pre[0 .. B] (pre[B] = total), by every thread of the workgroup; tmp holds
-// THREADS ints of scratch. Each thread takes up to 4 consecutive requests;
-// the per-thread sums are scanned in LDS (Hillis-Steele). Ends with a barrier.
+// pre[0 .. B] (pre[B] = total), by the first wave of the workgroup: lane l
+// takes requests [16 l, 16 l + 16) (B <= 1024), the lane sums are scanned
+// across the wave with shuffles, then every lane writes its requests' prefix
+// sums. Every thread of the workgroup calls it (it ends with a barrier).
 template <class C>
 __device__ void balanced_prefix(const FwdParams& p, const int32_t* lengths, int capacity,
-                                int32_t* pre, int32_t* tmp, int tid) {
-  const int per = (p.batch + C::THREADS - 1) / C::THREADS;  // <= 4
-  const int b0 = tid * per;
-  int cnt[4];
-  int local = 0;
+                                int32_t* pre, int wave, int lane) {
+  if (wave == 0) {
+    constexpr int kPer = kMaxBalancedBatch / 64;
+    const int b0 = lane * kPer;
+    int cnt[kPer];
+    int local = 0;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int b = b0 + i;
-    int c = 0;
-    if (i < per && b < p.batch) {
-      int len = lengths[b];
-      len = len < 0 ? 0 : (len > capacity ? capacity : len);
-      c = balanced_splits(len, p.split_keys, p.splits);
+    for (int i = 0; i < kPer; ++i) {
+      const int b = b0 + i;
+      int c = 0;
+      if (b < p.batch) {
+        int len = lengths[b];
+        len = len < 0 ? 0 : (len > capacity ? capacity : len);
+        c = balanced_splits(len, p.split_keys, p.splits);
+      }
+      cnt[i] = c;
+      local += c;
     }
-    cnt[i] = c;
-    local += c;
-  }
-  tmp[tid] = local;
-  __syncthreads();
-  for (int off = 1; off < C::THREADS; off <<= 1) {
-    const int add = tid >= off ? tmp[tid - off] : 0;
-    __syncthreads();
-    tmp[tid] += add;
-    __syncthreads();
-  }
-  int run = tmp[tid] - local;
+    int incl = local;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    if (i < per && b0 + i < p.batch) {
-      pre[b0 + i] = run;
-      run += cnt[i];
+    for (int off = 1; off < 64; off <<= 1) {
+      const int up = __shfl_up(incl, off, 64);
+      incl += lane >= off ? up : 0;
     }
+    int run = incl - local;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      if (b0 + i < p.batch) {
+        pre[b0 + i] = run;
+        run += cnt[i];
+      }
+    }
+    if (lane == 63) pre[p.batch] = incl;
   }
-  if (tid == C::THREADS - 1) pre[p.batch] = tmp[tid];
   __syncthreads();
 }
 
@@ -660,7 +659,7 @@ __global__ __launch_bounds__(C::THREADS) void fwd_kernel(FwdParams p,
   if constexpr (C::LAYOUT == kLayoutKey) {
     if (balanced) {
       balanced_prefix<C>(p, lengths, capacity, reinterpret_cast<int32_t*>(smem + C::PREFIX_OFF),
-                         reinterpret_cast<int32_t*>(smem), tid);
+                         wave, lane);
       work = __builtin_amdgcn_readfirstlane(pre[p.batch]) * p.heads * p.q_tiles;
     }
   }
@@ -668,10 +667,17 @@ __global__ __launch_bounds__(C::THREADS) void fwd_kernel(FwdParams p,
   if (p.mode == 2) {  // static schedule: this program's segments
     first = p.seg_offsets[prog];
     count = p.seg_offsets[prog + 1] - first;
-  } else {  // contiguous range of work items
-    const int per = work / grid, rem = work % grid;
-    first = prog * per + (prog < rem ? prog : rem);
-    count = per + (prog < rem ? 1 : 0);
+  } else if (work < grid && (int)blockIdx.x >= work) {
+    first = count = 0;  // a balanced plan with fewer live items than programs
+  } else {
+    // Contiguous ranges over the programs that have work: all of them, or,
+    // when a balanced plan has fewer live items than programs, the first
+    // `work` ones, which the hardware spreads over every XCD (i % 8).
+    const int active = work < grid ? work : grid;
+    const int aprog = active == grid ? prog : xcd_remap(blockIdx.x, active);
+    const int per = work / active, rem = work % active;
+    first = aprog * per + (aprog < rem ? aprog : rem);
+    count = per + (aprog < rem ? 1 : 0);
   }
 
   for (int it = 0; it < count; ++it) {

@@ -208,30 +208,39 @@ def test_wide_merge_many_splits():
 
 
 def test_length_balanced_splits():
-    """Ragged decode batches under the automatic split take length-balanced
-    splits (request b: clamp(ceil(len_b / split_keys), 1, S) slots). Outputs
-    against the oracle with NaN in every unread pool row; the partial and merge
-    components (the merge given the lengths) equal the fused call bit for bit;
-    with uniform lengths a balanced plan equals the even plan bit for bit."""
+    """Ragged decode batches with length-balanced splits (request b:
+    clamp(ceil(len_b / split_keys), 1, S) slots): the automatic split picks
+    them for config 4's imbalanced B4 at KV 32768; explicit plans cover the
+    rest. Outputs against the oracle with NaN in every unread pool row; the
+    partial and merge components (the merge given the lengths) equal the
+    fused call bit for bit; with uniform lengths a balanced plan equals the
+    even plan bit for bit."""
     from fgw_amd.operators.mha.current import build_kernel, mha_paged_decode
     cases = (("imbalanced_kv32768", 4, 1, 8, 128, 128, 256, [13321, 16319, 6592, 12115],
-              torch.bfloat16),
-             ("imbalanced_q16", 4, 16, 8, 128, 128, 64, [4635, 4285, 4326, 1917], torch.float16),
-             ("empty_and_short", 5, 1, 2, 128, 64, 64, [0, 4096, 17, 1000, 2500], torch.bfloat16),
-             ("page32_q7", 3, 7, 4, 128, 32, 64, [2048, 100, 1500], torch.bfloat16))
-    for (name, b, sq, h, d, page, width, lens, dtype) in cases:
+              torch.bfloat16, None),
+             ("imbalanced_q16", 4, 16, 8, 128, 128, 64, [4635, 4285, 4326, 1917], torch.float16,
+              (16, 491)),
+             ("empty_and_short", 5, 1, 2, 128, 64, 64, [0, 4096, 17, 1000, 2500], torch.bfloat16,
+              (16, 470)),
+             ("page32_q7", 3, 7, 4, 128, 32, 64, [2048, 100, 1500], torch.bfloat16, (32, 83)))
+    for (name, b, sq, h, d, page, width, lens, dtype, explicit) in cases:
         case = (name, b, sq, h, d, page, width)
         q, k, v, table = O.make_inputs(case, 5, dtype)
         lengths = torch.tensor(lens, dtype=torch.int32)
         k, v = O.poison_unread(k, v, table, lengths, page)
         dev = [x.cuda() for x in (q, k, v, table, lengths)]
-        got = mha_paged_decode(*dev, page_size=page)
+        dname = "bfloat16" if dtype == torch.bfloat16 else "float16"
+        if explicit is None:
+            got = mha_paged_decode(*dev, page_size=page)
+            kern = build_kernel(b, sq, h, d, k.shape[0], width, page, False, dname, 0,
+                                cache_lengths=tuple(lens))
+        else:
+            kern = build_kernel(b, sq, h, d, k.shape[0], width, page, False, dname, 0,
+                                num_splits=explicit[0], layout="key", split_keys=explicit[1])
+            got = kern(*dev)
         torch.cuda.synchronize()
         expected = O.reference(q, k, v, table, lengths, page, False)
         check_output(got, expected, q, lengths, False, f"balanced {name}")
-        dname = "bfloat16" if dtype == torch.bfloat16 else "float16"
-        kern = build_kernel(b, sq, h, d, k.shape[0], width, page, False, dname, 0,
-                            cache_lengths=tuple(lens))
         assert kern.split_balance == "length" and kern.split_keys > 0, (name, kern.num_splits)
         fused = kern(*dev)
         parts, lse = kern.partial_kernel(*dev)

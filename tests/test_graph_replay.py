@@ -102,7 +102,7 @@ def test_graph_replays_of_a_balanced_plan_with_new_lengths():
     q, k, v, table = O.make_inputs(case, 6, torch.bfloat16)
     first = [4635, 4285, 4326, 1917]
     kern = build_kernel(b, sq, h, d, k.shape[0], width, page, False, "bfloat16", 0,
-                        cache_lengths=tuple(first))
+                        num_splits=16, layout="key", split_keys=491)
     assert kern.split_balance == "length"
     dq, dk, dv, dt = (x.cuda() for x in (q, k, v, table))
     dl = torch.tensor(first, dtype=torch.int32, device="cuda")
