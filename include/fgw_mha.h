@@ -145,8 +145,9 @@ int fgw_mha_query_device(int device, fgw_mha_device_info* info);
 /* Validate a shape and resolve layout, split count and grid. Pure host
  * function (no HIP calls). Replaces the split selection and persistent-grid
  * arithmetic of build_kernel (v7.py:48-113; general_split_policy.py:9-21):
- * automatic splits double while B*H*q_tiles*splits leaves CU slots idle and
- * every split keeps at least two rounds of key blocks. Errors mirror the
+ * automatic splits double while B*H*q_tiles*(2 splits) still fits the
+ * device's resident workgroup slots and every split keeps at least two
+ * rounds of key blocks (four in the prefill layout). Errors mirror the
  * reference ValueErrors (v7.py:49-55, :97-99). */
 int fgw_mha_plan(const fgw_mha_shape* shape, const fgw_mha_request* request,
                  const fgw_mha_device_info* device, fgw_mha_plan_t* plan);
