@@ -162,16 +162,30 @@ __device__ __forceinline__ void issue_slow_tile(const FwdParams& p, const int32_
 // The wave's share of the K and V tiles of one block in the fast case (the
 // block lies in one page, below len, inside the pool, with D == DPAD):
 // uniform tile bases plus the wave's fixed per-lane offsets.
+// Per-lane byte offsets of the wave's DMA instructions from a block's first
+// row: the chunk offsets of DmaLanes plus the instruction's first row
+// (RPI i rows), so that every instruction of a block shares one uniform base.
+template <class C>
+struct BlockDma {
+  u32 k[C::INSTR_PER_WAVE], v[C::INSTR_PER_WAVE];
+  __device__ __forceinline__ BlockDma(const DmaLanes<C>& dl, int wave, int64_t row_bytes) {
+#pragma unroll
+    for (int q = 0; q < C::INSTR_PER_WAVE; ++q) {
+      const u32 rows = (u32)((int64_t)(C::RPI * (q * C::NWQ + wave)) * row_bytes);
+      k[q] = dl.kq(q, wave) + rows;
+      v[q] = dl.vq(q, wave) + rows;
+    }
+  }
+};
+
 template <class C>
 __device__ __forceinline__ void issue_fast_block(const char* kbase, const char* vbase, u32 kdst,
-                                                 u32 vdst, const DmaLanes<C>& dl, int wave,
-                                                 int64_t row_bytes) {
+                                                 u32 vdst, const BlockDma<C>& bd, int wave) {
 #pragma unroll
   for (int q = 0; q < C::INSTR_PER_WAVE; ++q) {
-    const int ii = q * C::NWQ + wave;
-    const int64_t rows = (int64_t)(C::RPI * ii) * row_bytes;
-    dma_saddr(kbase + rows, dl.kq(q, wave), kdst + 1024u * (u32)ii);
-    dma_saddr(vbase + rows, dl.vq(q, wave), vdst + 1024u * (u32)ii);
+    const u32 ii = (u32)(q * C::NWQ + wave);
+    dma_saddr(kbase, bd.k[q], kdst + 1024u * ii);
+    dma_saddr(vbase, bd.v[q], vdst + 1024u * ii);
   }
 }
 
@@ -274,6 +288,7 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p,
   const Lanes<C> ln(lane);
   const int64_t row_bytes = (int64_t)p.heads * p.dim * 2;
   const DmaLanes<C> dl(lane, wave, row_bytes);
+  const BlockDma<C> bd(dl, wave, row_bytes);
 
   const int grid = gridDim.x;
   const int prog = xcd_remap(blockIdx.x, grid);
@@ -343,7 +358,7 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p,
         const u32 kdst = kring_lds + (u32)((j % C::NKSLOT) * C::TILE_BYTES);
         const u32 vdst = vring_lds + (u32)((j % C::NVSLOT) * C::TILE_BYTES);
         if (off >= 0) {
-          issue_fast_block<C>(kb + off, vb + off, kdst, vdst, dl, wave, row_bytes);
+          issue_fast_block<C>(kb + off, vb + off, kdst, vdst, bd, wave);
         } else {
           issue_slow_tile<C, false>(p, table_b, kb, row_bytes, key0 + jc * C::BN, len, kdst, wave,
                                     lane);
