@@ -58,10 +58,12 @@ def parse():
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 1 GiB device copy (counter calibration) and exit")
     ap.add_argument("--suite", default="headline",
-                    choices=("headline", "decode-scan", "grid", "prefill", "static", "power",
-                             "scans"),
+                    choices=("headline", "decode-scan", "decode-batch", "grid", "prefill",
+                             "static", "power", "scans"),
                     help="headline: the one-line bench contract (default). decode-scan: "
-                         "config 4 split scan; grid: config 2 short-Q grid; "
+                         "config 4 split scan; decode-batch: Q1 decode split scan over larger "
+                         "batches and head counts (split cost model calibration); grid: "
+                         "config 2 short-Q grid; "
                          "prefill: Q4096 and Q32768; static: B1H1 static-plan path against "
                          "the automatic split path; power: MFMA rate on N(0,1) against "
                          "constant inputs (library GEMM and the headline kernel); scans: the "
@@ -202,7 +204,7 @@ def _checked(kern, dinputs, expected, dtype, label):
 
 def suite_decode_scan(args, emit):
     """Config 4: B2 H8 D128 page 128, Q in {1, 16} x KV in {512 .. 32768}, FP16 and
-    BF16, splits 1..64 and auto; plus the imbalanced B4 variant."""
+    BF16, splits 1..128 and auto; plus the imbalanced B4 variant."""
     import torch
     from fgw_amd.operators.mha.current import build_kernel
     from oracle import mha_oracle as O
@@ -215,7 +217,7 @@ def suite_decode_scan(args, emit):
                 dinputs = [x.to(dev) for x in host]
                 expected = O.chunked_reference(*host, page, False, 128)
                 nbytes = O.algorithmic_bytes([kv] * b, sq, h, d, kv // page)
-                for req in (None, 1, 2, 4, 8, 16, 32, 64):
+                for req in (None, 1, 2, 4, 8, 16, 32, 64, 128):
                     if req is not None and req > kv // 32:
                         continue
                     kern = build_kernel(b, sq, h, d, host[1].shape[0], kv // page, page, False,
@@ -260,6 +262,39 @@ def suite_decode_scan(args, emit):
                       "split_keys": kern.split_keys,
                       "grid": kern.compute_grid, "us_per_call": single, "us_back_to_back": back,
                       "hbm_gbs": nbytes / (single * 1e-6) / 1e9})
+
+
+def suite_decode_batch(args, emit):
+    """Q1 decode (D128 BF16, page 128, full cache) over larger batches and head
+    counts than config 4 (32 to 512 (b, h) tasks, 134-537 MB of K/V), splits
+    1..64 and auto: calibration data for the split cost model beyond B2 H8."""
+    import torch
+    from fgw_amd.operators.mha.current import build_kernel
+    from oracle import mha_oracle as O
+    dev = torch.device("cuda", 0)
+    d, page = 128, 128
+    for b, h, kv in ((4, 8, 32768), (8, 8, 16384), (8, 8, 4096), (4, 32, 8192), (16, 8, 8192),
+                     (8, 32, 4096), (32, 8, 2048), (16, 32, 2048), (64, 8, 1024)):
+        host = O.bench_inputs(b, 1, h, d, page, kv, torch.bfloat16)
+        dinputs = [x.to(dev) for x in host]
+        expected = O.chunked_reference(*host, page, False, 128)
+        nbytes = O.algorithmic_bytes([kv] * b, 1, h, d, kv // page)
+        for req in (None, 1, 2, 4, 8, 16, 32, 64):
+            if req is not None and req > kv // 32:
+                continue
+            kern = build_kernel(b, 1, h, d, host[1].shape[0], kv // page, page, False, "bfloat16",
+                                0, num_splits=req, full_kv_cache=True)
+            _checked(kern, dinputs, expected, torch.bfloat16, f"decode-batch B{b} H{h} kv{kv} "
+                                                              f"splits={req}")
+            single, back = _time_call(lambda: kern(*dinputs), args.scan_samples,
+                                      args.scan_warmup)
+            emit({"suite": "decode-batch", "dtype": "bf16", "batch": b, "heads": h,
+                  "head_dim": d, "q_len": 1, "kv_len": kv, "requested_splits": req,
+                  "num_splits": kern.num_splits, "grid": kern.compute_grid,
+                  "split_policy": kern.split_policy, "us_per_call": single,
+                  "us_back_to_back": back, "hbm_gbs": nbytes / (single * 1e-6) / 1e9})
+        del dinputs
+        torch.cuda.empty_cache()
 
 
 def suite_grid(args, emit):
@@ -429,7 +464,8 @@ def suite_power(args, emit):
 def run_scans(args):
     import torch
     torch.cuda.set_device(0)
-    suites = {"decode-scan": [suite_decode_scan], "grid": [suite_grid],
+    suites = {"decode-scan": [suite_decode_scan], "decode-batch": [suite_decode_batch],
+              "grid": [suite_grid],
               "prefill": [suite_prefill], "static": [suite_static], "power": [suite_power],
               "scans": [suite_prefill, suite_decode_scan, suite_grid, suite_static]}[args.suite]
     out = open(args.out, "w") if args.out else None
@@ -446,7 +482,8 @@ def run_scans(args):
     from fgw_amd.operators.mha.kernels.mha_paged_decode_hip import _device_info
     info = _device_info(0)
     emit({"suite": "device", "name": torch.cuda.get_device_properties(0).gcnArchName,
-          "num_cus": info.num_cus, "wg_per_cu": list(info.wg_per_cu)})
+          "num_cus": info.num_cus, "wg_per_cu": list(info.wg_per_cu),
+          "wg_per_cu_key_single": info.wg_per_cu_key_single})
     for fn in suites:
         fn(args, emit)
     if out:
@@ -496,6 +533,17 @@ def scan_markdown(records):
                          f"{r['us_per_call']:.1f} | {r['us_back_to_back']:.1f} | "
                          f"{r.get('partial_us', float('nan')):.1f} | "
                          f"{r.get('merge_us', float('nan')):.1f} | {r['hbm_gbs']:.0f} |")
+        lines.append("")
+    bat = [r for r in records if r["suite"] == "decode-batch"]
+    if bat:
+        lines += ["## Decode over larger batches (Q1 D128 BF16 page 128, full cache)", "",
+                  "| B | H | KV | splits | grid | us/call (single) | us (back-to-back) | "
+                  "GB/s (single) |", "|---|---|---|---|---|---|---|---|"]
+        for r in bat:
+            sp = f"auto->{r['num_splits']}" if r["requested_splits"] is None else str(r["num_splits"])
+            lines.append(f"| {r['batch']} | {r['heads']} | {r['kv_len']} | {sp} | {r['grid']} | "
+                         f"{r['us_per_call']:.1f} | {r['us_back_to_back']:.1f} | "
+                         f"{r['hbm_gbs']:.0f} |")
         lines.append("")
     imb = [r for r in records if r["suite"] == "decode-imbalanced"]
     if imb:

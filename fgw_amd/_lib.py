@@ -10,7 +10,7 @@ import pathlib
 import threading
 
 LIBRARY = pathlib.Path(__file__).resolve().with_name("libfgw_mha.so")
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 FGW_MHA_OK, FGW_MHA_EINVAL, FGW_MHA_EUNSUPPORTED, FGW_MHA_EHIP = 0, -1, -2, -3
 NOALLOC_SCRATCH_BYTES = 32 << 20  # FGW_MHA_NOALLOC_SCRATCH_BYTES
@@ -29,11 +29,12 @@ class Shape(ctypes.Structure):
 
 class Request(ctypes.Structure):
     _fields_ = [("num_splits", c_int32), ("persistent_programs", c_int32), ("layout", c_int32),
-                ("split_keys", c_int32)]
+                ("split_keys", c_int32), ("stages", c_int32)]
 
 
 class DeviceInfo(ctypes.Structure):
-    _fields_ = [("num_cus", c_int32), ("wg_per_cu", c_int32 * NUM_LAYOUTS), ("arch_gfx950", c_int32)]
+    _fields_ = [("num_cus", c_int32), ("wg_per_cu", c_int32 * NUM_LAYOUTS), ("arch_gfx950", c_int32),
+                ("wg_per_cu_key_single", c_int32)]
 
 
 class Plan(ctypes.Structure):
@@ -41,7 +42,8 @@ class Plan(ctypes.Structure):
                 ("num_splits", c_int32), ("query_tile_tasks", c_int32),
                 ("work_items", c_int32), ("grid", c_int32), ("threads", c_int32),
                 ("execution_mode", c_int32), ("dim_padded", c_int32),
-                ("parts_floats", c_int64), ("lse_floats", c_int64), ("split_keys", c_int32)]
+                ("parts_floats", c_int64), ("lse_floats", c_int64), ("split_keys", c_int32),
+                ("stages", c_int32)]
 
 
 class Tensors(ctypes.Structure):

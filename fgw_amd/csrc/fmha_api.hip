@@ -20,6 +20,8 @@ FGW_MHA_FOR_DPAD_LO(FGW_MHA_EXTERN, true)
 FGW_MHA_FOR_DPAD_HI(FGW_MHA_EXTERN, true)
 FGW_MHA_FOR_DPAD_LO(FGW_MHA_EXTERN, false)
 FGW_MHA_FOR_DPAD_HI(FGW_MHA_EXTERN, false)
+FGW_MHA_EXTERN_KEY_SINGLE(true)
+FGW_MHA_EXTERN_KEY_SINGLE(false)
 FGW_MHA_FOR_PREFILL_LO(FGW_MHA_EXTERN_PREFILL, true)
 FGW_MHA_FOR_PREFILL_HI(FGW_MHA_EXTERN_PREFILL, true)
 FGW_MHA_FOR_PREFILL_LO(FGW_MHA_EXTERN_PREFILL, false)
@@ -31,7 +33,12 @@ FGW_MHA_FOR_PREFILL_HI(FGW_MHA_EXTERN_PREFILL, false)
 #define FGW_PREFILL_ENTRY(BF, DP) \
   if (bf16 == BF && dpad == DP && layout == kLayoutPrefill) return FwdEntry{&launch_prefill<BF, DP>, &occupancy_prefill<BF, DP>};
 
-FwdEntry fwd_entry(bool bf16, int dpad, int layout) {
+FwdEntry fwd_entry(bool bf16, int dpad, int layout, int stages) {
+  if (stages == 1 && layout == kLayoutKey && dpad == 128)
+    return bf16 ? FwdEntry{&launch_fwd<true, 128, kLayoutKey, 1>,
+                           &occupancy_fwd<true, 128, kLayoutKey, 1>}
+                : FwdEntry{&launch_fwd<false, 128, kLayoutKey, 1>,
+                           &occupancy_fwd<false, 128, kLayoutKey, 1>};
   FGW_MHA_FOR_DPAD_LO(FGW_ENTRIES, true)
   FGW_MHA_FOR_DPAD_HI(FGW_ENTRIES, true)
   FGW_MHA_FOR_DPAD_LO(FGW_ENTRIES, false)
@@ -151,6 +158,28 @@ int scratch_address(int device, float** out) {
   return FGW_MHA_OK;
 }
 
+// K/V stages per key group of the default kernel of (layout, head-dim tile);
+// the prefill layout's rings have four slots.
+template <int LY>
+int cfg_stages(int dpad) {
+  switch (dpad) {
+    case 32: return Cfg<true, 32, LY>::NBUF;
+    case 64: return Cfg<true, 64, LY>::NBUF;
+    case 128: return Cfg<true, 128, LY>::NBUF;
+    default: return Cfg<true, 256, LY>::NBUF;
+  }
+}
+int default_stages(int layout, int dpad) {
+  if (layout == kLayoutPrefill) return 4;
+  return layout == kLayoutKey ? cfg_stages<kLayoutKey>(dpad) : cfg_stages<kLayoutQuery>(dpad);
+}
+// The key layout's single-stage variant exists for head-dim tile 128.
+bool has_key_single(int layout, int dpad) { return layout == kLayoutKey && dpad == 128; }
+bool stages_valid(int layout, int dpad, int stages) {
+  return stages == default_stages(layout, dpad) ||
+         (has_key_single(layout, dpad) && (stages == 1 || stages == 2));
+}
+
 // Keys one program consumes per loop round, and query rows per work item,
 // per layout.
 int keys_per_round(int layout) { return layout == kLayoutKey ? 4 * 32 : 64; }
@@ -225,7 +254,8 @@ int check_plan(const fgw_mha_shape* s, const fgw_mha_plan_t* p) {
       p->dim_padded != dim_tile(s->dim) || p->execution_mode != (p->num_splits > 1 ? 1 : 0) ||
       p->split_keys < 0 ||
       (p->split_keys > 0 && (p->layout != kLayoutKey || p->num_splits < 2 ||
-                             s->batch > kMaxBalancedBatch)))
+                             s->batch > kMaxBalancedBatch)) ||
+      !stages_valid(p->layout, p->dim_padded, p->stages))
     return fail(FGW_MHA_EINVAL, "plan does not match the shape; call fgw_mha_plan");
   return FGW_MHA_OK;
 }
@@ -299,7 +329,8 @@ int check_schedule(const fgw_mha_shape* s, const fgw_mha_schedule* sc) {
 
 int launch_partial_kernel(const fgw_mha_shape* s, const fgw_mha_plan_t* p,
                           const fgw_mha_tensors* t, int mode, hipStream_t stream) {
-  const FwdEntry e = fwd_entry(s->dtype == FGW_MHA_BFLOAT16, p->dim_padded, p->layout);
+  const int stages = p->stages == default_stages(p->layout, p->dim_padded) ? 0 : p->stages;
+  const FwdEntry e = fwd_entry(s->dtype == FGW_MHA_BFLOAT16, p->dim_padded, p->layout, stages);
   if (!e.launch) return fail(FGW_MHA_EUNSUPPORTED, "no kernel for dim tile %d", p->dim_padded);
   const FwdParams f = make_params(s, p, t, mode);
   const hipError_t err = e.launch(f, p->grid, stream);
@@ -348,6 +379,8 @@ int fgw_mha_query_device(int device, fgw_mha_device_info* info) {
     const int n = fwd_entry(true, 128, layout).occupancy();
     info->wg_per_cu[layout] = n > 0 ? n : 1;
   }
+  const int single = fwd_entry(true, 128, kLayoutKey, 1).occupancy();
+  info->wg_per_cu_key_single = single > 0 ? single : 1;
   if (current != device) (void)hipSetDevice(current);
   return FGW_MHA_OK;
 }
@@ -375,6 +408,11 @@ int fgw_mha_plan(const fgw_mha_shape* s, const fgw_mha_request* req,
   // KV tiles of 32 tokens, as the reference general route counts them
   // (cube_general.py:36); more splits than blocks leave empty splits.
   const int64_t kv_blocks = (capacity + 31) / 32;
+  if (req->stages != 0 && !stages_valid(layout, dpad, req->stages))
+    return fail(FGW_MHA_EINVAL,
+                "stages must be 0 (automatic), 1 or 2 for the key layout with head-dim tile "
+                "128, else 0 or %d", default_stages(layout, dpad));
+  const int wg_default = dev->wg_per_cu[layout] > 0 ? dev->wg_per_cu[layout] : 1;
 
   int splits = req->num_splits;
   if (splits != 0) {
@@ -385,14 +423,13 @@ int fgw_mha_plan(const fgw_mha_shape* s, const fgw_mha_request* req,
       return fail(FGW_MHA_EINVAL,
                   "num_splits must not exceed the number of KV tiles in table capacity");
   } else {
-    const int wg = dev->wg_per_cu[layout] > 0 ? dev->wg_per_cu[layout] : 1;
-    const int64_t slots = (int64_t)dev->num_cus * wg;
     const int rounds = layout == kLayoutPrefill ? kMinRoundsPerSplitPrefill : kMinRoundsPerSplit;
     const int64_t min_keys = (int64_t)keys_per_round(layout) * rounds;
     // Double while the doubled work items still fit the resident slots: one
     // doubling past them makes a second wave of items (B1H1 Q3712/KV4096:
     // 15 tiles x 32 splits = 480 items on 256 slots, 55.8 us, against 31.2 us
     // at 16 splits).
+    const int64_t slots = (int64_t)dev->num_cus * wg_default;
     splits = 1;
     while (splits < kAutoMaxSplits && tasks * splits * 2 <= slots &&
            (int64_t)(splits * 2) * min_keys <= capacity)
@@ -406,6 +443,18 @@ int fgw_mha_plan(const fgw_mha_shape* s, const fgw_mha_request* req,
                 "split_keys (length-balanced splits) needs the key layout, num_splits >= 2 and "
                 "B <= %d", kMaxBalancedBatch);
 
+  // Stages: the layout's default kernel unless the request names one. The key
+  // layout's single-stage kernel (head-dim tile 128, two workgroups per CU) is
+  // an explicit choice: measured faster only for long-cache decode split many
+  // ways (B2 H8 Q1 KV 32768: 64 splits on 512 programs 45.3 us against 47.1 us
+  // for 16 double-stage splits on 256), slower where a workgroup is alone on
+  // its CU (8 splits: 56.9 us against 47.7 us) and for large batches split a
+  // few ways (B8 H32 KV 4096, 2 splits: 115.9 us against 101.7 us at 1 split).
+  const int stages = req->stages != 0 ? req->stages : default_stages(layout, dpad);
+  const int wg_kernel = stages == 1 && has_key_single(layout, dpad)
+                            ? (dev->wg_per_cu_key_single > 0 ? dev->wg_per_cu_key_single : 1)
+                            : wg_default;
+
   int64_t grid = work;
   if (req->persistent_programs < -1)
     return fail(FGW_MHA_EINVAL, "persistent_programs must be -1, 0 or positive");
@@ -415,8 +464,7 @@ int fgw_mha_plan(const fgw_mha_shape* s, const fgw_mha_request* req,
     // Sq > len many are empty), so causal plans keep one workgroup per work
     // item and let the hardware dispatcher balance them: measured 1.06-2.5x
     // faster than the cap for causal prefill with more tiles than programs.
-    const int wg = dev->wg_per_cu[layout] > 0 ? dev->wg_per_cu[layout] : 1;
-    const int64_t cap = (int64_t)dev->num_cus * wg;
+    const int64_t cap = (int64_t)dev->num_cus * wg_kernel;
     grid = work < cap ? work : cap;
   } else if (req->persistent_programs > 0) {
     grid = work < req->persistent_programs ? work : req->persistent_programs;
@@ -435,6 +483,7 @@ int fgw_mha_plan(const fgw_mha_shape* s, const fgw_mha_request* req,
   out->parts_floats = splits > 1 ? (int64_t)s->batch * s->heads * splits * s->sq * s->dim : 0;
   out->lse_floats = splits > 1 ? (int64_t)s->batch * s->heads * splits * s->sq : 0;
   out->split_keys = req->split_keys;
+  out->stages = stages;
   return FGW_MHA_OK;
 }
 

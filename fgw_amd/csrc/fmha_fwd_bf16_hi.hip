@@ -5,5 +5,6 @@
 
 namespace fgw_mha {
 FGW_MHA_FOR_DPAD_HI(FGW_MHA_INSTANTIATE, true)
+FGW_MHA_INSTANTIATE_KEY_SINGLE(true)
 FGW_MHA_FOR_PREFILL_HI(FGW_MHA_INSTANTIATE_PREFILL, true)
 }  // namespace fgw_mha

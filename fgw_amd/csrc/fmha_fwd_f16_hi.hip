@@ -5,5 +5,6 @@
 
 namespace fgw_mha {
 FGW_MHA_FOR_DPAD_HI(FGW_MHA_INSTANTIATE, false)
+FGW_MHA_INSTANTIATE_KEY_SINGLE(false)
 FGW_MHA_FOR_PREFILL_HI(FGW_MHA_INSTANTIATE_PREFILL, false)
 }  // namespace fgw_mha

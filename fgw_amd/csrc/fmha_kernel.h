@@ -47,6 +47,12 @@
 //   kLayoutKey:   4 waves each stream their own 32-key blocks of the same 32
 //                 query rows (decode); the four partial softmax states are
 //                 combined through LDS before the epilogue.
+// Stages (template parameter STAGES, 0 = the default): K/V stages per key
+// group. Two keep the next block's DMA in flight while a block is computed;
+// the key layout's single-stage variant (head-dim tile 128) halves its LDS so
+// that two workgroups share a CU, one streaming while the other waits for its
+// DMA or runs its prologue and epilogue. The arithmetic is the same, so both
+// variants give the same bits.
 // Work items (b, h, q_tile, split) are spread over a persistent grid with
 // contiguous ranges per program (v7.py:260-264), after an XCD-aware remap of
 // the program id so that neighbouring items share an XCD's L2.
@@ -152,7 +158,7 @@ struct CMin {
   static constexpr int value = A < B ? A : B;
 };
 
-template <bool BF16_, int DPAD_, int LAYOUT_>
+template <bool BF16_, int DPAD_, int LAYOUT_, int STAGES_ = 0>
 struct Cfg {
   static constexpr bool BF16 = BF16_;
   static constexpr int DPAD = DPAD_;  // head dim padded to a power of two >= 32
@@ -172,7 +178,8 @@ struct Cfg {
   static constexpr int ROW_BYTES = DPAD * 2;
   static constexpr int TILE_BYTES = BN * ROW_BYTES;  // one K or V tile
   static constexpr int STAGE_BYTES = 2 * TILE_BYTES;
-  static constexpr int NBUF = NWK * 2 * STAGE_BYTES <= 128 * 1024 ? 2 : 1;
+  static constexpr int NBUF =
+      STAGES_ > 0 ? STAGES_ : (NWK * 2 * STAGE_BYTES <= 128 * 1024 ? 2 : 1);
   static constexpr int GROUP_BYTES = NBUF * STAGE_BYTES;
   static constexpr int TILES_BYTES = NWK * GROUP_BYTES;
   static constexpr int OSTRIDE = DPAD + 4;  // combine buffer row stride (floats)
@@ -195,6 +202,7 @@ struct Cfg {
   static_assert(NWQ == 1 || NWK == 1, "tiles are shared by all waves or by none");
   static_assert((DPAD & (DPAD - 1)) == 0 && DPAD >= 32 && DPAD <= 256, "head dim tile");
   static_assert(TILE_BYTES % 1024 == 0 && INSTR % NWQ == 0 && 64 % CPR == 0, "DMA granularity");
+  static_assert(NBUF == 1 || NBUF == 2, "one or two K/V stages per key group");
   static_assert(LDS_BYTES <= kLdsBudget, "LDS budget of one CU");
   static_assert(kMaxBalancedBatch % 64 == 0, "balanced-split prefix scan: whole lanes");
 };
@@ -889,17 +897,17 @@ __global__ __launch_bounds__(C::THREADS) void fwd_kernel(FwdParams p,
   }
 }
 
-template <bool BF16, int DPAD, int LAYOUT>
+template <bool BF16, int DPAD, int LAYOUT, int STAGES = 0>
 hipError_t launch_fwd(const FwdParams& p, int grid, hipStream_t stream) {
-  using C = Cfg<BF16, DPAD, LAYOUT>;
+  using C = Cfg<BF16, DPAD, LAYOUT, STAGES>;
   fwd_kernel<C><<<dim3(grid), dim3(C::THREADS), 0, stream>>>(p, p.table, p.lengths);
   return hipGetLastError();
 }
 
 // Resident workgroups per CU of one instantiation (0 if the query fails).
-template <bool BF16, int DPAD, int LAYOUT>
+template <bool BF16, int DPAD, int LAYOUT, int STAGES = 0>
 int occupancy_fwd() {
-  using C = Cfg<BF16, DPAD, LAYOUT>;
+  using C = Cfg<BF16, DPAD, LAYOUT, STAGES>;
   int n = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fwd_kernel<C>, C::THREADS, 0) != hipSuccess)
     return 0;

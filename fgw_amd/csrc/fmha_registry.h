@@ -22,7 +22,9 @@ inline int dim_tile(int dim) {
   return t;
 }
 
-FwdEntry fwd_entry(bool bf16, int dpad, int layout);
+// The kernel of (dtype, head-dim tile, layout, stages); stages 0 is the
+// instantiation's default, 1 the key layout's single-stage variant (tile 128).
+FwdEntry fwd_entry(bool bf16, int dpad, int layout, int stages = 0);
 hipError_t launch_merge(bool bf16, const MergeParams& p, hipStream_t stream);
 hipError_t launch_gather(const GatherParams& p, hipStream_t stream);
 hipError_t launch_pack(const PackParams& p, int total_pages, hipStream_t stream);
@@ -38,6 +40,13 @@ hipError_t launch_group_merge(bool bf16, const GroupMergeParams& p, int groups, 
   template hipError_t launch_fwd<BF, DP, kLayoutKey>(const FwdParams&, int, hipStream_t);   \
   template int occupancy_fwd<BF, DP, kLayoutQuery>();                                       \
   template int occupancy_fwd<BF, DP, kLayoutKey>();
+// The key layout's single-stage variant: head-dim tile 128 (two workgroups per CU).
+#define FGW_MHA_INSTANTIATE_KEY_SINGLE(BF)                                                  \
+  template hipError_t launch_fwd<BF, 128, kLayoutKey, 1>(const FwdParams&, int, hipStream_t); \
+  template int occupancy_fwd<BF, 128, kLayoutKey, 1>();
+#define FGW_MHA_EXTERN_KEY_SINGLE(BF)                                                              \
+  extern template hipError_t launch_fwd<BF, 128, kLayoutKey, 1>(const FwdParams&, int, hipStream_t); \
+  extern template int occupancy_fwd<BF, 128, kLayoutKey, 1>();
 // The prefill layout exists for head-dim tiles 64 and 128.
 #define FGW_MHA_FOR_PREFILL_LO(X, BF) X(BF, 64)
 #define FGW_MHA_FOR_PREFILL_HI(X, BF) X(BF, 128)

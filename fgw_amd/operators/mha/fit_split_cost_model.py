@@ -2,7 +2,7 @@
 
 Counterpart of the reference's fitting tools (tools/mha/fit_split_cost_model.py,
 tools/mha/fit_general_split_model.py): the calibration data are the JSONL
-records of `bench.py --suite decode-scan|grid --out FILE` (one record per
+records of `bench.py --suite decode-scan|decode-batch|grid --out FILE` (one record per
 (shape, split) with its measured single-call latency); the model is the
 linear score of split_cost_model.features.
 
@@ -35,7 +35,7 @@ from scipy.optimize import nnls
 
 from fgw_amd.operators.mha import split_cost_model as M
 
-SUITES = ("decode-scan", "decode-imbalanced", "grid")
+SUITES = ("decode-scan", "decode-batch", "decode-imbalanced", "grid")
 
 
 class _Device:

@@ -123,6 +123,9 @@ class _Launch(_launch.Launcher):
         self.execution_path = ROUTE
         self.layout = _LAYOUT_NAMES[plan.layout]
         self.dim_padded = plan.dim_padded
+        # K/V stages per key group of the selected kernel: 1 = the key layout's
+        # single-stage kernel (two workgroups per CU), 2 = double-stage.
+        self.stages = plan.stages
         # Q is read in place as [B, Sq, H, D]; no head-major copy is needed.
         self.prepare_q = lambda q: q
         if plan.execution_mode == 0:
@@ -207,7 +210,7 @@ class _Launch(_launch.Launcher):
 
 @lru_cache(maxsize=128)
 def _planned(batch, sq, heads, dim, pool_rows, width, page_size, causal, name, device_index,
-             splits, persistent, layout, meta, split_keys=0):
+             splits, persistent, layout, meta, split_keys=0, stages=0):
     """Launch callable of one (static shape, split request, grid request,
     layout): the unit the plan depends on. Ragged lengths reach the cost model
     before this cache, so a decode step with new lengths re-plans nothing
@@ -215,14 +218,15 @@ def _planned(batch, sq, heads, dim, pool_rows, width, page_size, causal, name, d
     device = _device_info(device_index)
     shape = _lib.Shape(batch, sq, heads, dim, pool_rows, width, page_size, int(bool(causal)),
                        _lib.DTYPE_BFLOAT16 if name == "bfloat16" else _lib.DTYPE_FLOAT16)
-    plan = _lib.plan(shape, _lib.Request(splits, persistent, _LAYOUTS[layout], split_keys), device)
+    plan = _lib.plan(shape, _lib.Request(splits, persistent, _LAYOUTS[layout], split_keys, stages),
+                     device)
     return _Launch(shape, plan, device_index, _DTYPES[name], dict(meta))
 
 
 def build_kernel(batch, sq, heads, dim, pool_rows, width, page_size, causal, dtype,
                  device_index=None, num_splits=None, split_policy="auto", full_kv_cache=False,
                  persistent_programs=PERSISTENT_DEVICE, cache_lengths=None, layout=None,
-                 split_keys=None):
+                 split_keys=None, stages=None):
     """Plan one static specialisation and return its launch callable.
 
     Arguments follow the reference build_kernel (v7.py:32-47) plus
@@ -234,13 +238,16 @@ def build_kernel(batch, sq, heads, dim, pool_rows, width, page_size, causal, dty
     alternate matrix and softmax phases, D in (32, 128]; "key" = waves split
     key blocks; None: key for Sq <= 32; prefill when its 256-row tiles fill
     the device, or, with KV splits, from Sq 1024, for D in (32, 128]; else
-    query), and split_keys (extra; with an explicit num_splits >= 2 and the
-    key layout: request b takes clamp(ceil(len_b / split_keys), 1, num_splits)
+    query), split_keys (extra; with an explicit num_splits >= 2 and the key
+    layout: request b takes clamp(ceil(len_b / split_keys), 1, num_splits)
     splits; the automatic split chooses it itself for ragged host-known
-    lengths). The reference caches build_kernel on its static arguments
-    (lru_cache(128), v7.py:32); here the split count is chosen first (the
-    cost model reads cache_lengths only under the auto/cost_model policy)
-    and the plans are cached per (shape, split count, grid, layout).
+    lengths) and stages (extra; K/V stages per key group: None = the
+    planner's choice, 1 or 2 = the key layout's single- or double-stage
+    kernel at head-dim tile 128). The reference caches build_kernel on its
+    static arguments (lru_cache(128), v7.py:32); here the split count is
+    chosen first (the cost model reads cache_lengths only under the
+    auto/cost_model policy) and the plans are cached per (shape, split count,
+    grid, layout, stages).
     """
     requested_split_policy = split_policy
     if split_policy not in SPLIT_POLICIES:
@@ -260,6 +267,9 @@ def build_kernel(batch, sq, heads, dim, pool_rows, width, page_size, causal, dty
     persistent = _persistent_request(persistent_programs)
     if layout not in _LAYOUTS:
         raise ValueError("layout must be None, 'query', 'key' or 'prefill'")
+    if stages is not None and stages not in (1, 2, 4):
+        raise ValueError("stages supports None (automatic), 1 or 2 (key layout, head-dim tile "
+                         "128) or the kernel's own count")
 
     if split_keys is not None and (type(split_keys) is not int or split_keys < 1
                                    or num_splits is None or num_splits < 2):
@@ -273,7 +283,8 @@ def build_kernel(batch, sq, heads, dim, pool_rows, width, page_size, causal, dty
             use_model = layout is None and split_cost_model.eligible_config(
                 batch, sq, heads, dim, width * page_size, page_size=page_size, causal=causal,
                 full_kv_cache=full_kv_cache, num_cus=device.num_cus,
-                lengths_known=cache_lengths is not None, wg_per_cu=tuple(device.wg_per_cu))
+                lengths_known=cache_lengths is not None,
+                wg_per_cu=split_cost_model.occupancy(device))
             split_policy = "cost_model" if use_model else "legacy"
         split_keys = 0
         if split_policy == "cost_model":
@@ -296,7 +307,7 @@ def build_kernel(batch, sq, heads, dim, pool_rows, width, page_size, causal, dty
     meta = (("persistent_programs", persistent_programs),
             ("requested_split_policy", requested_split_policy), ("split_policy", policy))
     return _planned(batch, sq, heads, dim, pool_rows, width, page_size, bool(causal), name,
-                    device_index, splits, persistent, layout, meta, split_keys)
+                    device_index, splits, persistent, layout, meta, split_keys, stages or 0)
 
 
 def mha_paged_decode(q, k_cache, v_cache, block_table, cache_seqlens, page_size, is_causal=False,

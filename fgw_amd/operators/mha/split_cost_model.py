@@ -13,8 +13,9 @@ Features of candidate s (layout and keys-per-round as the C planner uses:
 Sq <= 32 -> 4 key-parallel waves over 32 query rows, 128 keys per round;
 else 4 query-parallel waves over 128 rows, 64 keys per round):
   constant
-  wave_rounds      programs waves x key rounds of the longest split  (critical path)
-  waves            ceil(tasks * s / resident slots)
+  wave_rounds      ceil(tasks * s / CUs) x key rounds of the longest split
+                   (critical path of one CU: its resident programs share it)
+  waves            ceil(tasks * s / resident slots) (items one program runs)
   has_merge        s > 1
   partial_mbytes   s > 1: fp32 partial + LSE bytes written and read back, in MB
   merge_rows       s > 1: output rows merged x s / 1e3
@@ -43,17 +44,28 @@ def geometry(sq: int, dim: int = 128):
     return (1, 32, 128) if sq <= 32 else (0, 128, 64)
 
 
+def occupancy(device) -> tuple:
+    """Resident workgroups per CU of the query, key and prefill kernels
+    (fgw_mha_device_info.wg_per_cu)."""
+    return tuple(device.wg_per_cu)
+
+
 def features(batch, sq, heads, dim, lengths: Sequence[int], splits, num_cus, wg_per_cu):
     layout, rows, keys_round = geometry(sq, dim)
     tasks = batch * heads * math.ceil(sq / rows)
     slots = max(1, num_cus * max(1, wg_per_cu[layout]))
-    waves = math.ceil(tasks * splits / slots)
+    items = tasks * splits
+    waves = math.ceil(items / slots)
     rounds = [math.ceil(n / keys_round) for n in lengths]
     longest = math.ceil(max(rounds) / splits) if rounds else 0
     mean = (sum(rounds) / len(rounds)) / splits if rounds else 0.0
     multi = int(splits > 1)
     parts_mb = multi * batch * heads * splits * sq * (dim + 1) * 4 * 2 / 1e6
-    return [1.0, waves * longest * dim / 128.0, float(waves), float(multi), parts_mb,
+    # Critical path in key rounds per CU: the programs resident on one CU
+    # share its memory bandwidth and matrix cores, so a CU takes
+    # ceil(items / CUs) items of `longest` rounds whatever its slot count.
+    cu_rounds = math.ceil(items / num_cus) * longest
+    return [1.0, cu_rounds * dim / 128.0, float(waves), float(multi), parts_mb,
             multi * batch * heads * sq * splits / 1e3, max(0.0, longest - mean)]
 
 
@@ -161,7 +173,7 @@ def select_splits(batch, sq, heads, dim, capacity_tokens, lengths, device, model
         raise ValueError("No MI355X split cost model calibration is available; use split_policy='legacy'")
     if len(lengths) != batch or any(n < 0 or n > capacity_tokens for n in lengths):
         raise ValueError("cache_lengths must match batch and page-table capacity")
-    wg = tuple(device.wg_per_cu)
+    wg = occupancy(device)
     max_split = max(1, math.ceil(capacity_tokens / 32))
     costs = {s: predict(batch, sq, heads, dim, lengths, s, device.num_cus, wg, model)
              for s in SPLITS if s <= max_split}

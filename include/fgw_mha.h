@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define FGW_MHA_ABI_VERSION 4
+#define FGW_MHA_ABI_VERSION 5
 
 typedef enum {
   FGW_MHA_OK = 0,
@@ -85,6 +85,13 @@ typedef struct {
                                   clamp(ceil(len_b / split_keys), 1, num_splits) splits, so
                                   ragged requests get work items of similar size. No reference
                                   counterpart (the reference splits every request evenly). */
+  int32_t stages;              /* K/V stages per key group: 0 = the layout's default kernel
+                                  (double-stage for the key layout at head-dim tile 128);
+                                  1 or 2 selects the key layout's single-stage (two
+                                  workgroups per CU) or double-stage kernel where both exist
+                                  (head-dim tile 128); elsewhere only the kernel's own count
+                                  is accepted. No reference counterpart (a kernel-variant
+                                  choice). */
 } fgw_mha_request;
 
 /* Largest batch of a length-balanced split plan (split_keys > 0). */
@@ -95,6 +102,7 @@ typedef struct {
   int32_t num_cus;          /* compute units */
   int32_t wg_per_cu[FGW_MHA_NUM_LAYOUTS]; /* resident workgroups per CU, per layout, dim 128 */
   int32_t arch_gfx950;      /* 1 when the device is gfx950 */
+  int32_t wg_per_cu_key_single; /* the same for the key layout's single-stage kernel */
 } fgw_mha_device_info;
 
 /* Resolved launch plan: the attributes the reference launch callable
@@ -115,6 +123,8 @@ typedef struct {
   int32_t split_keys;      /* request.split_keys of a split plan (0: even splits); work_items and
                               the workspaces are then upper bounds, slot s of request b is used
                               for s < clamp(ceil(len_b / split_keys), 1, num_splits) */
+  int32_t stages;          /* K/V stages per key group of the selected kernel (query and key
+                              layouts; the prefill layout's rings have 4 slots: 4) */
 } fgw_mha_plan_t;
 
 /* Device buffers of one call. Workspaces are owned by the caller and sized
@@ -142,13 +152,15 @@ const char* fgw_mha_last_error(void);
  * torch.npu.get_device_properties(...).cube_core_num reads (v7.py:64-68, :104-108). */
 int fgw_mha_query_device(int device, fgw_mha_device_info* info);
 
-/* Validate a shape and resolve layout, split count and grid. Pure host
- * function (no HIP calls). Replaces the split selection and persistent-grid
- * arithmetic of build_kernel (v7.py:48-113; general_split_policy.py:9-21):
- * automatic splits double while B*H*q_tiles*(2 splits) still fits the
- * device's resident workgroup slots and every split keeps at least two
- * rounds of key blocks (four in the prefill layout). Errors mirror the
- * reference ValueErrors (v7.py:49-55, :97-99). */
+/* Validate a shape and resolve layout, split count, kernel stages and grid.
+ * Pure host function (no HIP calls). Replaces the split selection and
+ * persistent-grid arithmetic of build_kernel (v7.py:48-113;
+ * general_split_policy.py:9-21): automatic splits double while
+ * B*H*q_tiles*(2 splits) still fits the device's resident workgroup slots
+ * and every split keeps at least two rounds of key blocks (four in the
+ * prefill layout). Stages: the layout's default kernel unless requested; the
+ * persistent grid is capped at the selected kernel's resident slots. Errors
+ * mirror the reference ValueErrors (v7.py:49-55, :97-99). */
 int fgw_mha_plan(const fgw_mha_shape* shape, const fgw_mha_request* request,
                  const fgw_mha_device_info* device, fgw_mha_plan_t* plan);
 

@@ -11,7 +11,9 @@ from fgw_amd import _lib
 
 ROOT = pathlib.Path(__file__).resolve().parents[1]
 HEADER = ROOT / "include" / "fgw_mha.h"
-DEVICE = _lib.DeviceInfo(256, (ctypes.c_int32 * _lib.NUM_LAYOUTS)(2, 2, 1), 1)
+# MI355X: 256 CUs; resident workgroups per CU of the query, key and prefill
+# kernels (head-dim tile 128) and of the key layout's single-stage kernel.
+DEVICE = _lib.DeviceInfo(256, (ctypes.c_int32 * _lib.NUM_LAYOUTS)(2, 1, 1), 1, 2)
 
 
 @pytest.fixture(scope="module")
@@ -61,8 +63,9 @@ def test_plan_headline_shapes(lib):
     narrow = _lib.plan(shape(sq=4096, kv=2048, d=32), _lib.Request(0, -1, -1), DEVICE)
     assert narrow.layout == 0
     decode = _lib.plan(shape(sq=1, kv=32768), _lib.Request(0, -1, -1), DEVICE)
-    assert (decode.layout, decode.rows_per_tile, decode.num_splits, decode.work_items) == (1, 32, 32, 512)
-    assert decode.parts_floats == 2 * 8 * 32 * 1 * 128 and decode.lse_floats == 2 * 8 * 32
+    assert (decode.layout, decode.rows_per_tile, decode.num_splits, decode.work_items) == (1, 32, 16, 256)
+    assert (decode.stages, decode.grid) == (2, 256)
+    assert decode.parts_floats == 2 * 8 * 16 * 1 * 128 and decode.lse_floats == 2 * 8 * 16
     big = _lib.plan(shape(sq=32768, kv=2048), _lib.Request(0, -1, -1), DEVICE)
     assert big.layout == 2 and big.work_items == 2 * 8 * 128
     assert big.grid == 256  # persistent cap = 256 CUs x 1 program
@@ -115,6 +118,36 @@ def test_plan_length_balanced_splits(lib):
     big.pool_rows = 1025 * 8192
     with pytest.raises(ValueError, match="split_keys"):
         _lib.plan(big, _lib.Request(16, -1, _lib.LAYOUT_KEY, 600), DEVICE)
+
+
+def test_plan_kernel_stages(lib):
+    """Stages: the layout's default kernel unless requested. The key layout at
+    head-dim tile 128 has a single-stage kernel (two workgroups per CU) beside
+    its double-stage default; other kernels accept only their own count; the
+    grid cap follows the selected kernel."""
+    plan = lambda s, splits=0, stages=0: _lib.plan(  # noqa: E731
+        s, _lib.Request(splits, -1, -1, 0, stages), DEVICE)
+    for splits in (8, 16, 64):
+        assert (plan(shape(), splits).stages, plan(shape(), splits).grid) == (2, min(16 * splits, 256))
+    assert (plan(shape(), 64, 1).stages, plan(shape(), 64, 1).grid) == (1, 512)
+    assert (plan(shape(), 8, 1).stages, plan(shape(), 8, 1).grid) == (1, 128)
+    assert (plan(shape(), 64, 2).stages, plan(shape(), 64, 2).grid) == (2, 256)
+    assert plan(shape(), 0, 1).num_splits == plan(shape()).num_splits  # splits do not move
+    # Other kernels have one stage count: accepted when requested, else refused.
+    assert plan(shape(d=64)).stages == 2 and plan(shape(d=256)).stages == 1
+    assert plan(shape(d=256), 0, 1).stages == 1
+    assert plan(shape(sq=128, kv=2048), 0, 2).stages == 2  # query layout
+    assert plan(shape(sq=4096, kv=2048)).stages == 4  # prefill rings
+    for s, stages in ((shape(d=64), 1), (shape(d=256), 2), (shape(sq=128, kv=2048), 1),
+                      (shape(sq=4096, kv=2048), 2), (shape(), 3)):
+        with pytest.raises(ValueError, match="stages"):
+            plan(s, 0, stages)
+    # A plan with a stage count the kernel does not have is refused before any launch.
+    bad = _lib.Plan.from_buffer_copy(plan(shape(), 16))
+    bad.stages = 3
+    s, t = shape(), _lib.Tensors(16, 32, 48, 64, 80, 96, 112, 128)
+    rc = lib.fgw_mha_fwd(ctypes.byref(s), ctypes.byref(bad), ctypes.byref(t), None)
+    assert rc == _lib.FGW_MHA_EINVAL and b"plan" in lib.fgw_mha_last_error()
 
 
 @pytest.mark.parametrize("field,value,message", [

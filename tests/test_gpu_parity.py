@@ -264,6 +264,43 @@ def test_length_balanced_splits():
     assert torch.equal(balanced(*dev), even(*dev))
 
 
+def test_key_layout_stage_variants():
+    """The key layout's single-stage kernel (two workgroups per CU) and its
+    double-stage kernel (head-dim tile 128) give the same bits for every plan,
+    and the oracle's output: even and length-balanced splits, direct plans,
+    ragged, empty and causal rows, FP16 and BF16, head dims 96 and 128."""
+    from fgw_amd.operators.mha.current import build_kernel
+    cases = (
+        # name, B, Sq, H, D, page, width, dtype, lengths, causal, split_keys
+        ("decode_kv8192", 2, 1, 8, 128, 128, 64, torch.bfloat16, "full", False, None),
+        ("q5_ragged_causal", 3, 5, 2, 128, 16, 64, torch.float16, [1000, 0, 4], True, None),
+        ("q32_d96", 2, 32, 3, 96, 32, 24, torch.bfloat16, [768, 31], False, None),
+        ("balanced", 4, 1, 8, 128, 128, 64, torch.bfloat16, [4635, 0, 8192, 1917], False, 491),
+    )
+    for (name, b, sq, h, d, page, width, dtype, lens, causal, split_keys) in cases:
+        case = (name, b, sq, h, d, page, width)
+        q, k, v, table = O.make_inputs(case, 9, dtype)
+        lens = O.lengths_for(case, lens, 9) if isinstance(lens, str) else lens
+        lengths = torch.tensor(lens, dtype=torch.int32)
+        k, v = O.poison_unread(k, v, table, lengths, page)
+        dev = [x.cuda() for x in (q, k, v, table, lengths)]
+        dname = "bfloat16" if dtype == torch.bfloat16 else "float16"
+        expected = O.reference(q, k, v, table, lengths, page, causal)
+        for splits in ((16,) if split_keys else (1, 4, 16)):
+            outs = {}
+            for stages in (1, 2):
+                kern = build_kernel(b, sq, h, d, k.shape[0], width, page, causal, dname, 0,
+                                    num_splits=splits, layout="key", split_keys=split_keys,
+                                    stages=stages)
+                assert kern.stages == stages and kern.layout == "key", (name, stages)
+                outs[stages] = kern(*dev)
+            torch.cuda.synchronize()
+            label = f"stages {name} splits={splits}"
+            log(label)
+            check_output(outs[1], expected, q, lengths, causal, label)
+            assert torch.equal(outs[1], outs[2]), f"{label}: the two kernels differ in bits"
+
+
 def test_headline_shapes():
     from fgw_amd.operators.mha.current import build_kernel
     for (b, sq, h, d, p, kv) in ((1, 1, 1, 128, 128, 512), (2, 4096, 8, 128, 128, 2048),
