@@ -268,7 +268,9 @@ def test_key_layout_stage_variants():
     """The key layout's single-stage kernel (two workgroups per CU) and its
     double-stage kernel (head-dim tile 128) give the same bits for every plan,
     and the oracle's output: even and length-balanced splits, direct plans,
-    ragged, empty and causal rows, FP16 and BF16, head dims 96 and 128."""
+    several work items per program (64 splits of B2 H8: 1024 items on 512
+    single-stage programs), ragged, empty and causal rows, FP16 and BF16, head
+    dims 96 and 128."""
     from fgw_amd.operators.mha.current import build_kernel
     cases = (
         # name, B, Sq, H, D, page, width, dtype, lengths, causal, split_keys
@@ -286,13 +288,17 @@ def test_key_layout_stage_variants():
         dev = [x.cuda() for x in (q, k, v, table, lengths)]
         dname = "bfloat16" if dtype == torch.bfloat16 else "float16"
         expected = O.reference(q, k, v, table, lengths, page, causal)
-        for splits in ((16,) if split_keys else (1, 4, 16)):
+        for splits in ((16,) if split_keys else (1, 4, 16, 64)):
             outs = {}
+            if splits * 32 > width * page:
+                continue
             for stages in (1, 2):
                 kern = build_kernel(b, sq, h, d, k.shape[0], width, page, causal, dname, 0,
                                     num_splits=splits, layout="key", split_keys=split_keys,
                                     stages=stages)
                 assert kern.stages == stages and kern.layout == "key", (name, stages)
+                if name == "decode_kv8192" and splits == 64:
+                    assert kern.compute_grid == (512 if stages == 1 else 256), kern.compute_grid
                 outs[stages] = kern(*dev)
             torch.cuda.synchronize()
             label = f"stages {name} splits={splits}"
