@@ -410,8 +410,8 @@ int fgw_mha_plan(const fgw_mha_shape* s, const fgw_mha_request* req,
   const int64_t kv_blocks = (capacity + 31) / 32;
   if (req->stages != 0 && !stages_valid(layout, dpad, req->stages))
     return fail(FGW_MHA_EINVAL,
-                "stages must be 0 (automatic), 1 or 2 for the key layout with head-dim tile "
-                "128, else 0 or %d", default_stages(layout, dpad));
+                "stages must be 0 (the default kernel), 1 or 2 for the key layout with head-dim "
+                "tile 128, else 0 or %d", default_stages(layout, dpad));
   const int wg_default = dev->wg_per_cu[layout] > 0 ? dev->wg_per_cu[layout] : 1;
 
   int splits = req->num_splits;

@@ -242,8 +242,8 @@ def build_kernel(batch, sq, heads, dim, pool_rows, width, page_size, causal, dty
     layout: request b takes clamp(ceil(len_b / split_keys), 1, num_splits)
     splits; the automatic split chooses it itself for ragged host-known
     lengths) and stages (extra; K/V stages per key group: None = the
-    planner's choice, 1 or 2 = the key layout's single- or double-stage
-    kernel at head-dim tile 128). The reference caches build_kernel on its
+    layout's default kernel, 1 or 2 = the key layout's single- or
+    double-stage kernel at head-dim tile 128). The reference caches build_kernel on its
     static arguments (lru_cache(128), v7.py:32); here the split count is
     chosen first (the cost model reads cache_lengths only under the
     auto/cost_model policy) and the plans are cached per (shape, split count,
@@ -268,8 +268,8 @@ def build_kernel(batch, sq, heads, dim, pool_rows, width, page_size, causal, dty
     if layout not in _LAYOUTS:
         raise ValueError("layout must be None, 'query', 'key' or 'prefill'")
     if stages is not None and stages not in (1, 2, 4):
-        raise ValueError("stages supports None (automatic), 1 or 2 (key layout, head-dim tile "
-                         "128) or the kernel's own count")
+        raise ValueError("stages supports None (the default kernel), 1 or 2 (key layout, "
+                         "head-dim tile 128) or the kernel's own count")
 
     if split_keys is not None and (type(split_keys) is not int or split_keys < 1
                                    or num_splits is None or num_splits < 2):
