@@ -4,7 +4,9 @@ Each case draws B, H, D (16..256 in steps of 16), page size, table width, Q
 length, ragged lengths, causal, dtype, split request and layout from a fixed
 seed, poisons every unread pool row with NaN and checks the output against
 the oracle at the reference tolerances, with exactly-zero rows where no key
-is visible. The draws stay small enough for the oracle to finish in seconds.
+is visible. Key-layout plans at head-dim tile 128 also run on the
+single-stage key kernel, which must give the same bits. The draws stay small
+enough for the oracle to finish in seconds.
 """
 import random
 
@@ -51,7 +53,14 @@ def test_random_case(i):
     kern = build_kernel(b, sq, h, d, k.shape[0], width, page, causal,
                         "float16" if dtype == torch.float16 else "bfloat16", 0,
                         num_splits=splits, layout=layout, cache_lengths=tuple(lengths))
-    got = kern(*[x.cuda() for x in (q, k, v, table, lt)])
+    dev = [x.cuda() for x in (q, k, v, table, lt)]
+    got = kern(*dev)
+    if kern.layout == "key" and kern.dim_padded == 128:
+        # The single-stage key kernel computes the same bits.
+        single = build_kernel(b, sq, h, d, k.shape[0], width, page, causal,
+                              "float16" if dtype == torch.float16 else "bfloat16", 0,
+                              num_splits=kern.num_splits, layout="key", stages=1)
+        assert single.stages == 1 and torch.equal(single(*dev), got), label
     torch.cuda.synchronize()
     expected = O.reference(q, k, v, table, lt, page, causal)
     got = got.cpu()
@@ -104,6 +113,11 @@ def test_random_balanced_case(i):
     got = kern(*dev)
     parts, lse = kern.partial_kernel(*dev)
     merged = kern.merge_kernel(parts, lse, dev[4])
+    if kern.dim_padded == 128:
+        single = build_kernel(b, sq, h, d, k.shape[0], width, page, causal,
+                              "float16" if dtype == torch.float16 else "bfloat16", 0,
+                              num_splits=splits, layout="key", split_keys=split_keys, stages=1)
+        assert single.stages == 1 and torch.equal(single(*dev), got), label
     torch.cuda.synchronize()
     assert torch.equal(merged, got), label
     expected = O.reference(q, k, v, table, lt, page, causal)
