@@ -47,3 +47,38 @@ def test_full_size_rows_and_page_placement(b, sq, h, kv):
     expected = O.chunked_reference(q[:, rows].contiguous(), k, v, table, lengths, page, False, 128)
     rtol, atol = O.TOLERANCES[torch.bfloat16]
     torch.testing.assert_close(got[:, rows], expected, rtol=rtol, atol=atol)
+
+
+@pytest.mark.parametrize("sq,layout", [(1, None), (16, None), (96, "query"), (1024, None)])
+def test_pages_beyond_4_gib_into_the_pool(sq, layout):
+    """64-bit pool addressing: the same pages placed more than 4 GiB (K and V
+    each) into a large pool, the table shifted with them, give the same bits
+    as in a small pool; decode (key layout), query and prefill layouts. The
+    rest of the large pool is never written (uninitialised memory the
+    kernels must not read)."""
+    from fgw_amd.operators.mha.current import build_kernel
+    b, h, d, page, kv = 2, 8, 128, 128, 4096
+    q, k, v, table, lengths = O.bench_inputs(b, sq, h, d, page, kv, torch.bfloat16)
+    rows = k.shape[0]
+    row_bytes = h * d * 2
+    shift_pages = -(-(9 << 29) // (page * row_bytes))  # 4.5 GiB of rows, whole pages
+    shift = shift_pages * page
+    dq, dl = q.cuda(), lengths.cuda()
+    small = build_kernel(b, sq, h, d, rows, kv // page, page, False, "bfloat16", 0,
+                         full_kv_cache=True, layout=layout)
+    want = small(dq, k.cuda(), v.cuda(), table.cuda(), dl)
+    big_k = torch.empty(shift + rows, h, d, dtype=torch.bfloat16, device="cuda")
+    big_v = torch.empty_like(big_k)
+    big_k[shift:].copy_(k)
+    big_v[shift:].copy_(v)
+    big = build_kernel(b, sq, h, d, shift + rows, kv // page, page, False, "bfloat16", 0,
+                       full_kv_cache=True, layout=layout)
+    print(f"pool offset {shift * row_bytes / 2**30:.2f} GiB: Sq{sq} layout={big.layout} "
+          f"splits={big.num_splits}", flush=True)
+    assert (big.layout, big.num_splits) == (small.layout, small.num_splits)
+    got = big(dq, big_k, big_v, (table + shift_pages).cuda(), dl)
+    torch.cuda.synchronize()
+    assert shift * row_bytes > 4 << 30
+    assert torch.equal(got, want), "output depends on the pool offset"
+    del big_k, big_v
+    torch.cuda.empty_cache()
