@@ -300,6 +300,10 @@ def test_key_layout_stage_variants():
                 if name == "decode_kv8192" and splits == 64:
                     assert kern.compute_grid == (512 if stages == 1 else 256), kern.compute_grid
                 outs[stages] = kern(*dev)
+                if stages == 1 and splits > 1:  # the component calls run the same kernel
+                    parts, lse = kern.partial_kernel(*dev)
+                    merged = kern.merge_kernel(parts, lse, dev[4] if split_keys else None)
+                    assert torch.equal(merged, outs[1]), f"{name} splits={splits} components"
             torch.cuda.synchronize()
             label = f"stages {name} splits={splits}"
             log(label)
