@@ -16,25 +16,28 @@ namespace fgw_mha {
 // all-empty row is exactly zero.
 constexpr int kMergeChunk = 16;
 // One (row, 4 dims): split s's LSE at ls[s * lse_stride], its part at
-// ps[s * part_stride]; the result goes to dst in the input dtype.
-template <bool BF16>
-__device__ __forceinline__ void merge_one(const float* ls, int64_t lse_stride, const float* ps,
-                                          int64_t part_stride, int splits, u16* dst) {
+// ps[s * part_stride]; the result goes to dst in the input dtype. Chunks of
+// CH splits; the loads of a chunk's missing splits past `splits` are
+// clamped to the last split and carry weight 0.
+template <bool BF16, int CH>
+__device__ __forceinline__ void merge_one_chunked(const float* ls, int64_t lse_stride,
+                                                  const float* ps, int64_t part_stride,
+                                                  int splits, u16* dst) {
   using E = Elem<BF16>;
   float peak = kNegBig, tot = 0.0f;
   f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int s0 = 0; s0 < splits; s0 += kMergeChunk) {
-    float x[kMergeChunk];
-    f32x4 v[kMergeChunk];
+  for (int s0 = 0; s0 < splits; s0 += CH) {
+    float x[CH];
+    f32x4 v[CH];
 #pragma unroll
-    for (int i = 0; i < kMergeChunk; ++i) {
+    for (int i = 0; i < CH; ++i) {
       const int s = s0 + i < splits ? s0 + i : splits - 1;  // clamped; weight 0 below
       x[i] = ls[(int64_t)s * lse_stride];
       v[i] = *reinterpret_cast<const f32x4*>(ps + (int64_t)s * part_stride);
     }
     float cpeak = peak;
 #pragma unroll
-    for (int i = 0; i < kMergeChunk; ++i) {
+    for (int i = 0; i < CH; ++i) {
       const bool live = s0 + i < splits && x[i] > -1.0e29f;
       cpeak = live ? fmaxf(cpeak, x[i]) : cpeak;
     }
@@ -42,7 +45,7 @@ __device__ __forceinline__ void merge_one(const float* ls, int64_t lse_stride, c
     tot *= keep;
     acc *= keep;
 #pragma unroll
-    for (int i = 0; i < kMergeChunk; ++i) {
+    for (int i = 0; i < CH; ++i) {
       const bool live = s0 + i < splits && x[i] > -1.0e29f;
       const float wgt = live ? expf(x[i] - cpeak) : 0.0f;
       tot += wgt;
@@ -55,6 +58,24 @@ __device__ __forceinline__ void merge_one(const float* ls, int64_t lse_stride, c
   w.x = E::pack2(acc[0] * inv, acc[1] * inv);
   w.y = E::pack2(acc[2] * inv, acc[3] * inv);
   *reinterpret_cast<u32x2*>(dst) = w;
+}
+
+// merge_one_chunked with the smallest chunk of 2, 4, 8 or 16 that holds all
+// `splits` (one chunk up to 16): a chunk of 16 for 2 splits would issue
+// eight times the loads (the clamped ones), which the prefill-length merges
+// of few splits feel. The live splits are summed in the same order whatever
+// the chunk (a larger chunk only adds zeros for its dead splits).
+template <bool BF16>
+__device__ __forceinline__ void merge_one(const float* ls, int64_t lse_stride, const float* ps,
+                                          int64_t part_stride, int splits, u16* dst) {
+  if (splits <= 2)
+    merge_one_chunked<BF16, 2>(ls, lse_stride, ps, part_stride, splits, dst);
+  else if (splits <= 4)
+    merge_one_chunked<BF16, 4>(ls, lse_stride, ps, part_stride, splits, dst);
+  else if (splits <= 8)
+    merge_one_chunked<BF16, 8>(ls, lse_stride, ps, part_stride, splits, dst);
+  else
+    merge_one_chunked<BF16, kMergeChunk>(ls, lse_stride, ps, part_stride, splits, dst);
 }
 
 // Splits row (b, ., .) of a merge reads: all slots, or the balanced count
