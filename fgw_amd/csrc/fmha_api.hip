@@ -188,21 +188,23 @@ int rows_per_tile(int layout) {
 }
 // Head-dim tiles with a prefill-layout kernel.
 bool has_prefill(int dpad) { return dpad == 64 || dpad == 128; }
-// The automatic layout choice takes the prefill layout
-//  - when its 256-row query tiles alone give every resident program of the
-//    device a work item (measured faster than the query layout: B2 H8 D128
-//    BF16, KV 2048, Q 4096 and Q 32768);
-//  - for fewer tiles, where KV splits fill the device, from Q 1024 on:
-//    measured with the automatic splits of both layouts (B1-B4, H8-H16,
-//    KV 2048-8192, head-dim tiles 64 and 128, causal or not) the prefill
-//    layout is 1.06-1.25x faster there (on par at Q 512).
-// Shorter cases keep the query layout.
+// The automatic layout choice takes the prefill layout for Q longer than one
+// query-layout tile (Sq > 128) when its 256-row query tiles alone give every
+// resident program of the device a work item, when Sq >= 1024, or when the
+// work B * H * Sq * capacity reaches 2^24 query-key pairs. Measured over 250 seeded shapes (B 1-16, H 8-32, head-dim tiles 64 and
+// 128, Sq 64-2048, capacity 1024-16384, causal or not), each layout at its
+// best split count, as the query layout's time over the prefill layout's:
+// Sq > 128 from 2^24 pairs on 0.996-1.54 (1.24 geometric mean, 173
+// shapes); 2^23-2^24 pairs 0.90-1.07 (even); below 2^23 pairs 0.89-1.0
+// (the query layout's shorter work items win); Sq <= 128, where a 256-row
+// tile is at least half padding, 0.76-1.05 (0.94).
 bool auto_prefill(const fgw_mha_shape* s, const fgw_mha_device_info* dev, int dpad) {
-  if (!has_prefill(dpad) || s->sq < 256) return false;
+  if (!has_prefill(dpad) || s->sq <= 128) return false;
   const int rows = 256;
   const int64_t tiles = (int64_t)s->batch * s->heads * ((s->sq + rows - 1) / rows);
   const int wg = dev->wg_per_cu[kLayoutPrefill] > 0 ? dev->wg_per_cu[kLayoutPrefill] : 1;
-  return tiles >= (int64_t)dev->num_cus * wg || s->sq >= 1024;
+  const int64_t pairs = (int64_t)s->batch * s->heads * s->sq * ((int64_t)s->width * s->page_size);
+  return tiles >= (int64_t)dev->num_cus * wg || s->sq >= 1024 || pairs >= (int64_t(1) << 24);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -424,7 +426,14 @@ int fgw_mha_plan(const fgw_mha_shape* s, const fgw_mha_request* req,
                   "num_splits must not exceed the number of KV tiles in table capacity");
   } else {
     const int rounds = layout == kLayoutPrefill ? kMinRoundsPerSplitPrefill : kMinRoundsPerSplit;
-    const int64_t min_keys = (int64_t)keys_per_round(layout) * rounds;
+    int64_t min_keys = (int64_t)keys_per_round(layout) * rounds;
+    // Prefill layout: a split also takes at least 8 keys per query tile task.
+    // Each doubling adds a partial row per task row to write and merge, while
+    // the keys of a split shrink; with many tasks the merge outweighs the
+    // shorter items (B1 H16 Q1536 KV 1024, 96 tasks: 32.5 us unsplit against
+    // 39.6 us at 2 splits). Measured over 160 seeded shapes: 1.006x the best
+    // split count on geometric mean, against 1.012x with 256 keys alone.
+    if (layout == kLayoutPrefill && 8 * tasks > min_keys) min_keys = 8 * tasks;
     // Double while the doubled work items still fit the resident slots: one
     // doubling past them makes a second wave of items (B1H1 Q3712/KV4096:
     // 15 tiles x 32 splits = 480 items on 256 slots, 55.8 us, against 31.2 us

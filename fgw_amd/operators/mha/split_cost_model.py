@@ -83,18 +83,20 @@ def load_model(path: str = str(MODEL_PATH)) -> Optional[dict]:
     return model
 
 
-def planner_takes_prefill(batch, sq, heads, dim, num_cus, wg_per_cu) -> bool:
+def planner_takes_prefill(batch, sq, heads, dim, num_cus, wg_per_cu, kv_tokens) -> bool:
     """True where fgw_mha_plan's automatic layout is the prefill layout (256-row
-    tiles, fmha_api.hip auto_prefill): head-dim tile 64 or 128, Sq >= 256, and
-    either Sq >= 1024 or its tiles alone fill the device. geometry() does not
-    describe that kernel, so the model is not used there."""
+    tiles, fmha_api.hip auto_prefill): head-dim tile 64 or 128, Sq > 128, and
+    its tiles alone fill the device, Sq >= 1024, or B * H * Sq * kv_tokens (the
+    table capacity) reaches 2^24. geometry() does not describe that kernel, so
+    the model is not used there."""
     dpad = 32
     while dpad < dim:
         dpad *= 2
-    if dpad not in (64, 128) or sq < 256:
+    if dpad not in (64, 128) or sq <= 128:
         return False
     wg = max(1, wg_per_cu[2]) if wg_per_cu is not None else 1
-    return sq >= 1024 or batch * heads * math.ceil(sq / 256) >= num_cus * wg
+    return (sq >= 1024 or batch * heads * math.ceil(sq / 256) >= num_cus * wg
+            or batch * heads * sq * kv_tokens >= 1 << 24)
 
 
 def eligible_config(batch, sq, heads, dim, kv_tokens, *, page_size, causal, full_kv_cache,
@@ -110,7 +112,7 @@ def eligible_config(batch, sq, heads, dim, kv_tokens, *, page_size, causal, full
     return (not causal and num_cus == scope["num_cus"] and (full_kv_cache or lengths_known)
             and scope["min_kv"] <= kv_tokens <= scope["max_kv"]
             and scope["min_sq"] <= sq <= scope["max_sq"] and dim in scope["dims"]
-            and not planner_takes_prefill(batch, sq, heads, dim, num_cus, wg_per_cu))
+            and not planner_takes_prefill(batch, sq, heads, dim, num_cus, wg_per_cu, kv_tokens))
 
 
 def predict(batch, sq, heads, dim, lengths, splits, num_cus, wg_per_cu, model) -> float:

@@ -43,6 +43,23 @@ def shape(b=2, sq=1, h=8, d=128, kv=32768, page=128, causal=0, dtype=_lib.DTYPE_
     return _lib.Shape(b, sq, h, d, b * width * page, width, page, causal, dtype)
 
 
+def test_cost_model_guard_matches_the_planner_layout(lib):
+    # split_cost_model.planner_takes_prefill restates fgw_mha_plan's automatic
+    # prefill-layout rule; the split cost model must never be used for shapes
+    # the planner runs on the prefill kernel.
+    from fgw_amd.operators.mha import split_cost_model as M
+    wg = tuple(DEVICE.wg_per_cu)
+    for b in (1, 2, 16):
+        for h in (1, 8, 32):
+            for sq in (1, 32, 33, 128, 129, 200, 255, 256, 384, 512, 1023, 1024, 4096):
+                for d in (32, 64, 96, 128, 192):
+                    for kv in (128, 1000, 2048, 8192, 65536):
+                        p = _lib.plan(shape(b=b, h=h, sq=sq, d=d, kv=kv), _lib.Request(0, -1, -1), DEVICE)
+                        width = (kv + 127) // 128
+                        want = M.planner_takes_prefill(b, sq, h, d, DEVICE.num_cus, wg, width * 128)
+                        assert (p.layout == 2) == want, (b, h, sq, d, kv)
+
+
 def test_plan_headline_shapes(lib):
     # 2 x 8 x 16 prefill tiles of 256 rows fill the 256 CUs: prefill layout.
     prefill = _lib.plan(shape(sq=4096, kv=2048), _lib.Request(0, -1, -1), DEVICE)
@@ -52,10 +69,18 @@ def test_plan_headline_shapes(lib):
     mid = _lib.plan(shape(sq=128, kv=2048), _lib.Request(0, -1, -1), DEVICE)
     assert (mid.layout, mid.rows_per_tile, mid.threads) == (0, 128, 256)  # short Q: query layout
     # 64 prefill tiles, KV splits fill the device: prefill layout from Q 1024 (head-dim
-    # tiles 64 and 128, causal or not); Q 512 keeps the query layout.
+    # tiles 64 and 128, causal or not), and for Q > 128 from 2^24 query-key pairs
+    # (B x H x Sq x capacity); splits of at least 8 keys per task (512 here).
     few = _lib.plan(shape(sq=1024, kv=2048), _lib.Request(0, -1, -1), DEVICE)
     assert (few.layout, few.q_tiles, few.num_splits, few.work_items) == (2, 4, 4, 256)
-    assert _lib.plan(shape(sq=512, kv=2048), _lib.Request(0, -1, -1), DEVICE).layout == 0
+    assert _lib.plan(shape(sq=512, kv=2048), _lib.Request(0, -1, -1), DEVICE).layout == 2
+    assert _lib.plan(shape(sq=512, kv=1024), _lib.Request(0, -1, -1), DEVICE).layout == 0
+    assert _lib.plan(shape(sq=129, kv=8192), _lib.Request(0, -1, -1), DEVICE).layout == 2
+    assert _lib.plan(shape(sq=128, kv=32768), _lib.Request(0, -1, -1), DEVICE).layout == 0
+    # 96 tasks: 768 keys per split at least, so KV 1024 stays unsplit (the fill
+    # rule of 256 keys alone took 2 splits).
+    tall = _lib.plan(shape(b=1, h=16, sq=1536, kv=1024), _lib.Request(0, -1, -1), DEVICE)
+    assert (tall.layout, tall.q_tiles, tall.num_splits) == (2, 6, 1)
     assert _lib.plan(shape(sq=1024, kv=2048, causal=1), _lib.Request(0, -1, -1), DEVICE).layout == 2
     assert _lib.plan(shape(sq=1024, kv=2048, d=64), _lib.Request(0, -1, -1), DEVICE).layout == 2
     wide = _lib.plan(shape(sq=4096, kv=2048, d=256), _lib.Request(0, -1, -1), DEVICE)
