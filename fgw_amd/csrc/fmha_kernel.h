@@ -567,6 +567,76 @@ __device__ __forceinline__ void store_row(const FwdParams& p, int b, int h, int 
   }
 }
 
+// Output rows of one wave through LDS (D == DPAD >= 64). Lane (il, hh) holds
+// row il's dims 32 dt + 8 gq + 4 hh + i in o[dt][4 gq + i]; stored directly,
+// each store instruction scatters 8-16 bytes per lane over 32 rows. The wave
+// instead writes its 32 rows into `st` (its own 32 * kStagedRowBytes<C> bytes
+// of LDS, which no other wave touches meanwhile), reads them back as 16-byte
+// chunks of whole rows and stores 2-8 full rows per instruction. The 16-byte
+// chunk c of staged row r sits at chunk c ^ (r % chunks per row), so both
+// the column writes of 32 rows and the row reads spread over all banks.
+// bf16/fp16 rows (f32 false) go to bdst + r * brow_stride bytes, all DPAD
+// dims in one pass; fp32 rows (f32 true) to fdst + r * DPAD floats, 64 dims
+// (256 bytes per row) per pass. Rows r >= rows are not stored.
+template <class C>
+constexpr int kStagedRowBytes = 2 * C::DPAD > 256 ? 2 * C::DPAD : 256;
+
+template <class C>
+__device__ __forceinline__ void store_rows_staged(unsigned char* st, int lane,
+                                                  const f32x16 (&o)[C::DT], float inv, bool f32,
+                                                  float* fdst, unsigned char* bdst,
+                                                  int64_t brow_stride, int rows) {
+  using E = Elem<C::BF16>;
+  static_assert(C::DPAD >= 64 && C::DPAD % 64 == 0, "staged rows need D tiles of 64k");
+  // The lane id passes through an opaque copy so that the compiler cannot
+  // hoist the staging addresses (functions of the lane alone) out of the
+  // work-item loop, where they would stay live across the main loop.
+  asm volatile("v_mov_b32 %0, %1" : "=v"(lane) : "v"(lane));
+  const int il = lane & 31, hh = lane >> 5;
+  if (f32) {
+    constexpr int RB = 256, NCH = RB / 16, RPI = 64 / NCH;
+#pragma unroll
+    for (int pass = 0; pass < C::DPAD / 64; ++pass) {
+#pragma unroll
+      for (int dt2 = 0; dt2 < 2; ++dt2)
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+          const int dt = 2 * pass + dt2, c = 8 * dt2 + 2 * gq + hh;
+          f32x4 val = {o[dt][4 * gq], o[dt][4 * gq + 1], o[dt][4 * gq + 2], o[dt][4 * gq + 3]};
+          *reinterpret_cast<f32x4*>(st + il * RB + 16 * (c ^ (il % NCH))) = val * inv;
+        }
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int k = 0; k < 32 / RPI; ++k) {
+        const int r = RPI * k + lane / NCH, c = lane % NCH;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(st + r * RB + 16 * (c ^ (r % NCH)));
+        if (r < rows)
+          *reinterpret_cast<u32x4*>(fdst + (int64_t)r * C::DPAD + 64 * pass + 4 * c) = v;
+      }
+      __builtin_amdgcn_wave_barrier();  // the next pass rewrites the region
+    }
+  } else {
+    constexpr int RB = C::DPAD * 2, NCH = RB / 16, RPI = 64 / NCH;
+#pragma unroll
+    for (int dt = 0; dt < C::DT; ++dt)
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        const int c = 4 * dt + gq;
+        u32x2 w;
+        w.x = E::pack2(o[dt][4 * gq] * inv, o[dt][4 * gq + 1] * inv);
+        w.y = E::pack2(o[dt][4 * gq + 2] * inv, o[dt][4 * gq + 3] * inv);
+        *reinterpret_cast<u32x2*>(st + il * RB + 16 * (c ^ (il % NCH)) + 8 * hh) = w;
+      }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int k = 0; k < 32 / RPI; ++k) {
+      const int r = RPI * k + lane / NCH, c = lane % NCH;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(st + r * RB + 16 * (c ^ (r % NCH)));
+      if (r < rows) *reinterpret_cast<u32x4*>(bdst + r * brow_stride + 16 * c) = v;
+    }
+  }
+}
+
 __device__ __forceinline__ float lse_of(float m_log2, float total) {
   return total > 0.0f ? (m_log2 + log2f(total)) * kLn2 : kNegBig;
 }
@@ -832,7 +902,10 @@ __global__ __launch_bounds__(C::THREADS) void fwd_kernel(FwdParams p,
     wait_dma();  // no DMA of this work item outlives it
     if constexpr (C::NWK == 1) {
       const float tot = pair_sum(l);
-      if (qrow < p.sq) {
+      // Direct stores: D < DPAD, or D tiles below 128 (staged, D tile 64
+      // measured 1.3% slower on two query-layout shapes).
+      auto store_direct = [&]() {
+        if (qrow >= p.sq) return;
         const float inv = 1.0f / fmaxf(tot, 1.0e-30f);
 #pragma unroll
         for (int dt = 0; dt < C::DT; ++dt)
@@ -844,11 +917,39 @@ __global__ __launch_bounds__(C::THREADS) void fwd_kernel(FwdParams p,
               store_row<C>(p, b, h, split, qrow, d0, val, inv, slot, q0);
             }
           }
-        if (p.mode == 1 && hh == 0) {
-          p.lse[(((int64_t)b * p.heads + h) * p.splits + split) * p.sq + qrow] = lse_of(m, tot);
-        } else if (p.mode == 2 && slot >= 0 && hh == 0) {
-          p.lse[(int64_t)slot * C::ROWS_TILE + (qrow - q0)] = lse_of(m, tot);
+      };
+      if constexpr (C::DPAD >= 128) {
+        if (p.dim == C::DPAD) {
+          // Every wave's DMA into the stages has landed (each waited for its
+          // own above) and no wave reads them any more: they stage the output.
+          __syncthreads();
+          static_assert(C::NWQ * 32 * kStagedRowBytes<C> <= C::TILES_BYTES,
+                        "staged rows fit the K/V stages");
+          const bool f32 = p.mode == 1 || (p.mode == 2 && slot >= 0);
+          float* fdst = nullptr;
+          if (p.mode == 1)
+            fdst = p.parts +
+                   ((((int64_t)b * p.heads + h) * p.splits + split) * p.sq + row_base) * C::DPAD;
+          else if (f32)
+            fdst = p.parts + ((int64_t)slot * C::ROWS_TILE + (row_base - q0)) * C::DPAD;
+          unsigned char* bdst =
+              f32 ? nullptr
+                  : static_cast<unsigned char*>(p.out) +
+                        (((int64_t)b * p.sq + row_base) * p.heads + h) * C::DPAD * 2;
+          store_rows_staged<C>(smem + wq * 32 * kStagedRowBytes<C>, lane, o,
+                               1.0f / fmaxf(tot, 1.0e-30f), f32, fdst, bdst,
+                               (int64_t)p.heads * C::DPAD * 2, p.sq - row_base);
+        } else {
+          store_direct();
         }
+      } else {
+        store_direct();
+      }
+      if (qrow < p.sq && hh == 0) {
+        if (p.mode == 1)
+          p.lse[(((int64_t)b * p.heads + h) * p.splits + split) * p.sq + qrow] = lse_of(m, tot);
+        else if (p.mode == 2 && slot >= 0)
+          p.lse[(int64_t)slot * C::ROWS_TILE + (qrow - q0)] = lse_of(m, tot);
       }
     } else {
       // Combine the NWK key-group states of the same query rows.

@@ -271,82 +271,6 @@ __device__ __forceinline__ void matrix_phase(const OperandAddr<C>& ad, u32 koff,
   __builtin_amdgcn_s_setprio(0);
 }
 
-// Output of one wave's 32 query rows (row_base ..) through LDS, for D == DPAD.
-// Lane (il, hh) holds O[row_base + il][32 dt + 8 gq + 4 hh + i] in
-// o[dt][4 gq + i]; stored directly, each store instruction would scatter
-// 8-16 bytes per lane over 32 rows. Each wave instead writes its rows into
-// its own 32-row region of the (then idle) K/V rings, reads them back as
-// 16-byte chunks of whole rows and stores 4-8 full rows per instruction.
-// The 16-byte chunk c of staged row r sits at chunk c ^ (r % chunks per row),
-// so the column writes of 32 rows and the row reads both spread over all
-// banks. bf16/fp16 outputs stage all DPAD dims at once (DPAD * 2 bytes per
-// row); fp32 partials (mode 1) stage 64 dims (256 bytes per row) per pass.
-// The caller has passed a workgroup barrier after every wave's last DMA into
-// the rings landed.
-template <class C>
-__device__ __forceinline__ void store_tile_staged(const FwdParams& p, unsigned char* smem,
-                                                  int wave, int lane, int b, int h, int split,
-                                                  int row_base, const f32x16 (&o)[C::DT],
-                                                  float inv) {
-  using E = Elem<C::BF16>;
-  static_assert(C::WAVES * 32 * 256 <= C::LDS_BYTES && C::WAVES * 32 * C::DPAD * 2 <= C::LDS_BYTES,
-                "staged rows fit the rings");
-  // The lane id passes through an opaque copy so that the compiler cannot
-  // hoist the staging addresses (functions of the lane alone) out of the
-  // work-item loop, where they would stay live across the main loop.
-  asm volatile("v_mov_b32 %0, %1" : "=v"(lane) : "v"(lane));
-  const int il = lane & 31, hh = lane >> 5;
-  if (p.mode == 1) {
-    constexpr int RB = 256, NCH = RB / 16, RPI = 64 / NCH;
-    unsigned char* st = smem + wave * 32 * RB;
-    float* dst = p.parts +
-                 ((((int64_t)b * p.heads + h) * p.splits + split) * p.sq + row_base) * C::DPAD;
-#pragma unroll
-    for (int pass = 0; pass < C::DPAD / 64; ++pass) {
-#pragma unroll
-      for (int dt2 = 0; dt2 < 2; ++dt2)
-#pragma unroll
-        for (int gq = 0; gq < 4; ++gq) {
-          const int dt = 2 * pass + dt2, c = 8 * dt2 + 2 * gq + hh;
-          f32x4 val = {o[dt][4 * gq], o[dt][4 * gq + 1], o[dt][4 * gq + 2], o[dt][4 * gq + 3]};
-          *reinterpret_cast<f32x4*>(st + il * RB + 16 * (c ^ (il % NCH))) = val * inv;
-        }
-      __builtin_amdgcn_wave_barrier();
-#pragma unroll
-      for (int k = 0; k < 32 / RPI; ++k) {
-        const int r = RPI * k + lane / NCH, c = lane % NCH;
-        const u32x4 v = *reinterpret_cast<const u32x4*>(st + r * RB + 16 * (c ^ (r % NCH)));
-        if (row_base + r < p.sq)
-          *reinterpret_cast<u32x4*>(dst + (int64_t)r * C::DPAD + 64 * pass + 4 * c) = v;
-      }
-      __builtin_amdgcn_wave_barrier();  // the next pass rewrites the region
-    }
-  } else {
-    constexpr int RB = C::DPAD * 2, NCH = RB / 16, RPI = 64 / NCH;
-    unsigned char* st = smem + wave * 32 * RB;
-#pragma unroll
-    for (int dt = 0; dt < C::DT; ++dt)
-#pragma unroll
-      for (int gq = 0; gq < 4; ++gq) {
-        const int c = 4 * dt + gq;
-        u32x2 w;
-        w.x = E::pack2(o[dt][4 * gq] * inv, o[dt][4 * gq + 1] * inv);
-        w.y = E::pack2(o[dt][4 * gq + 2] * inv, o[dt][4 * gq + 3] * inv);
-        *reinterpret_cast<u32x2*>(st + il * RB + 16 * (c ^ (il % NCH)) + 8 * hh) = w;
-      }
-    __builtin_amdgcn_wave_barrier();
-    const int64_t row_stride = (int64_t)p.heads * C::DPAD * 2;
-    unsigned char* dst = static_cast<unsigned char*>(p.out) +
-                         (((int64_t)b * p.sq + row_base) * p.heads + h) * C::DPAD * 2;
-#pragma unroll
-    for (int k = 0; k < 32 / RPI; ++k) {
-      const int r = RPI * k + lane / NCH, c = lane % NCH;
-      const u32x4 v = *reinterpret_cast<const u32x4*>(st + r * RB + 16 * (c ^ (r % NCH)));
-      if (row_base + r < p.sq) *reinterpret_cast<u32x4*>(dst + r * row_stride + 16 * c) = v;
-    }
-  }
-}
-
 template <class C>
 __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p,
                                                              const int32_t* __restrict__ table,
@@ -543,8 +467,18 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p,
       // Every wave's DMA into the rings has landed (each waited for its own
       // above) and no wave reads them any more: the rings stage the output.
       __syncthreads();
-      store_tile_staged<C>(p, smem, wave, lane, b, h, split, row_base, o,
-                           1.0f / fmaxf(tot, 1.0e-30f));
+      static_assert(C::WAVES * 32 * kStagedRowBytes<C> <= C::LDS_BYTES, "staged rows fit the rings");
+      const bool f32 = p.mode == 1;
+      float* fdst =
+          f32 ? p.parts + ((((int64_t)b * p.heads + h) * p.splits + split) * p.sq + row_base) *
+                              C::DPAD
+              : nullptr;
+      unsigned char* bdst = f32 ? nullptr
+                                : static_cast<unsigned char*>(p.out) +
+                                      (((int64_t)b * p.sq + row_base) * p.heads + h) * C::DPAD * 2;
+      store_rows_staged<C>(smem + wave * 32 * kStagedRowBytes<C>, lane, o,
+                           1.0f / fmaxf(tot, 1.0e-30f), f32, fdst, bdst,
+                           (int64_t)p.heads * C::DPAD * 2, p.sq - row_base);
       if (p.mode == 1 && hh == 0 && qrow < p.sq)
         p.lse[(((int64_t)b * p.heads + h) * p.splits + split) * p.sq + qrow] = lse_of(m, tot);
     } else if (qrow < p.sq) {
