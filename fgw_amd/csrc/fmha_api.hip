@@ -434,6 +434,16 @@ int fgw_mha_plan(const fgw_mha_shape* s, const fgw_mha_request* req,
     // 39.6 us at 2 splits). Measured over 160 seeded shapes: 1.006x the best
     // split count on geometric mean, against 1.012x with 256 keys alone.
     if (layout == kLayoutPrefill && 8 * tasks > min_keys) min_keys = 8 * tasks;
+    // Query layout: four rounds (256 keys) once B * H * Sq * capacity reaches
+    // 2^22 pairs. Over 84 seeded multi-head shapes of the query layout's range
+    // (Sq 48-1023, causal or not, head-dim tiles 64 and 128) this is 1.009x
+    // the best split count on geometric mean for D 128 and 1.020x otherwise,
+    // against 1.040x and 1.057x at two rounds (B2 H8 Q96 KV4096 D64: 26.1 us
+    // at 32 splits, 17.7 us at 16); single-head B1 shapes below 2^22 pairs keep
+    // two rounds (four cost them 1.15x).
+    const int64_t pairs = (int64_t)s->batch * s->heads * s->sq * capacity;
+    if (layout == kLayoutQuery && pairs >= (int64_t(1) << 22) && min_keys < 4 * 64)
+      min_keys = 4 * 64;
     // Double while the doubled work items still fit the resident slots: one
     // doubling past them makes a second wave of items (B1H1 Q3712/KV4096:
     // 15 tiles x 32 splits = 480 items on 256 slots, 55.8 us, against 31.2 us

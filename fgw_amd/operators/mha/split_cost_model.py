@@ -99,6 +99,16 @@ def planner_takes_prefill(batch, sq, heads, dim, num_cus, wg_per_cu, kv_tokens) 
             or batch * heads * sq * kv_tokens >= 1 << 24)
 
 
+def planner_fill_preferred(batch, sq, heads, kv_tokens) -> bool:
+    """Query-layout shapes (Sq > 32) of at least 2^22 query-key pairs
+    (B * H * Sq * table capacity), where fgw_mha_plan's own fill rule (four key
+    rounds per split there) measured closer to the best split count than the
+    model: 1.009x against 1.041x on geometric mean over 40 multi-head D128
+    shapes (the model's query-layout calibration is the single-head B1 H1
+    grid)."""
+    return sq > 32 and batch * heads * sq * kv_tokens >= 1 << 22
+
+
 def eligible_config(batch, sq, heads, dim, kv_tokens, *, page_size, causal, full_kv_cache,
                     num_cus, lengths_known=False, wg_per_cu=None) -> bool:
     """Automatic policy guard: the calibrated scope of the frozen model (non-causal,
@@ -112,7 +122,8 @@ def eligible_config(batch, sq, heads, dim, kv_tokens, *, page_size, causal, full
     return (not causal and num_cus == scope["num_cus"] and (full_kv_cache or lengths_known)
             and scope["min_kv"] <= kv_tokens <= scope["max_kv"]
             and scope["min_sq"] <= sq <= scope["max_sq"] and dim in scope["dims"]
-            and not planner_takes_prefill(batch, sq, heads, dim, num_cus, wg_per_cu, kv_tokens))
+            and not planner_takes_prefill(batch, sq, heads, dim, num_cus, wg_per_cu, kv_tokens)
+            and not planner_fill_preferred(batch, sq, heads, kv_tokens))
 
 
 def predict(batch, sq, heads, dim, lengths, splits, num_cus, wg_per_cu, model) -> float:

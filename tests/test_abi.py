@@ -77,6 +77,11 @@ def test_plan_headline_shapes(lib):
     assert _lib.plan(shape(sq=512, kv=1024), _lib.Request(0, -1, -1), DEVICE).layout == 0
     assert _lib.plan(shape(sq=129, kv=8192), _lib.Request(0, -1, -1), DEVICE).layout == 2
     assert _lib.plan(shape(sq=128, kv=32768), _lib.Request(0, -1, -1), DEVICE).layout == 0
+    # Query layout: 4 key rounds (256 keys) per split from 2^22 pairs, else 2 rounds.
+    q96 = _lib.plan(shape(sq=96, d=64, kv=4096), _lib.Request(0, -1, -1), DEVICE)
+    assert (q96.layout, q96.num_splits) == (0, 16)  # 16 tasks; 32 splits would be 128 keys
+    q64 = _lib.plan(shape(b=1, h=1, sq=64, kv=4096), _lib.Request(0, -1, -1), DEVICE)
+    assert (q64.layout, q64.num_splits) == (0, 32)  # 2^18 pairs: 128 keys per split
     # 96 tasks: 768 keys per split at least, so KV 1024 stays unsplit (the fill
     # rule of 256 keys alone took 2 splits).
     tall = _lib.plan(shape(b=1, h=16, sq=1536, kv=1024), _lib.Request(0, -1, -1), DEVICE)

@@ -83,6 +83,12 @@ def test_eligibility_scope(model):
                              lengths_known=True, **kw)
     assert not M.eligible_config(2, 1, 8, 128, 8192, causal=False, full_kv_cache=True,
                                  page_size=128, num_cus=304)
+    # Query-layout shapes from 2^22 query-key pairs use the planner's fill rule.
+    assert M.eligible_config(1, 64, 1, 128, 4096, causal=False, full_kv_cache=True, **kw)
+    assert M.eligible_config(1, 256, 1, 128, 8192, causal=False, full_kv_cache=True, **kw)
+    assert not M.eligible_config(1, 256, 1, 128, 16384, causal=False, full_kv_cache=True, **kw)
+    assert not M.eligible_config(2, 64, 8, 128, 8192, causal=False, full_kv_cache=True, **kw)
+    assert M.eligible_config(16, 16, 32, 128, 16384, causal=False, full_kv_cache=True, **kw)
 
 
 def test_select_rejects_bad_lengths(model):
