@@ -728,6 +728,7 @@ def main():
     decode = {"workload": "Q1/KV32768 B2H8 D128 BF16 page128", "us_per_call": d_med * 1e3,
               "us_per_call_min": min(d_single) * 1e3, "gbs": dbytes / (d_med * 1e-3) / 1e9,
               "us_back_to_back": d_back * 1e3, "bytes": dbytes, "num_splits": dkern.num_splits,
+              "stages": dkern.stages,
               "split_policy": dkern.split_policy, "grid": dkern.compute_grid,
               "execution_mode": dkern.execution_mode,
               "roofline_call": {"bound": "hbm", "kernel": "whole call (every kernel, single-call "
@@ -738,7 +739,10 @@ def main():
         pcall = lambda: dkern.partial_kernel(*dinputs)  # noqa: E731
         p_ms = region_ms(pcall, args.steps, args.warmup) / args.steps
         p_achieved = dbytes / (p_ms * 1e-3) / 1e9
-        decode["roofline"] = {"bound": "hbm", "kernel": "fwd_kernel (partial, key layout)",
+        stage_name = "single-stage" if dkern.stages == 1 else "double-stage"
+        decode["roofline"] = {"bound": "hbm",
+                              "kernel": f"fwd_kernel (partial, key layout, {stage_name}, "
+                                        f"{dkern.num_splits} splits)",
                               "achieved": p_achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                               "frac": p_achieved / PEAK_HBM_GBS,
                               "traffic": traffic_from_profile("decode_partial"),

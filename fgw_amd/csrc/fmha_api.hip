@@ -175,6 +175,26 @@ int default_stages(int layout, int dpad) {
 }
 // The key layout's single-stage variant exists for head-dim tile 128.
 bool has_key_single(int layout, int dpad) { return layout == kLayoutKey && dpad == 128; }
+
+// Automatic plans of short decode (Sq <= 4) on the key layout at head-dim
+// tile 128 whose even splits number 16 or more and give each CU at most one
+// work item move to the single-stage kernel with 4x the splits (each keeping
+// >= 512 keys), else 2x (>= 256 keys); returns that split count, or 0 to keep
+// the plan. Two workgroups per CU then overlap one's prologue and epilogue
+// with the other's stream. Measured (single-call median, same box, A/B):
+// B2 H8 KV 32768 0.962-0.965x (BF16 and FP16), KV 65536 0.975x, KV 16384
+// 0.981x, KV 8192 0.972x, B1 H8 / B2 H4 KV 32768 0.993x, B1 H16 Q4 0.987x;
+// below 16 splits (B2 H16 or B8 H8, 4-8 splits) and at Sq 16 it measured
+// 1.00-1.05x, so those plans stay.
+int single_stage_splits(const fgw_mha_shape* s, const fgw_mha_device_info* dev, int layout,
+                        int dpad, int64_t tasks, int splits, int64_t capacity) {
+  if (!has_key_single(layout, dpad) || s->sq > 4 || splits < 16 ||
+      dev->wg_per_cu_key_single < 2 || tasks * splits > dev->num_cus)
+    return 0;
+  if (4 * splits <= kMaxSplits && capacity / (4 * splits) >= 512) return 4 * splits;
+  if (2 * splits <= kMaxSplits && capacity / (2 * splits) >= 256) return 2 * splits;
+  return 0;
+}
 bool stages_valid(int layout, int dpad, int stages) {
   return stages == default_stages(layout, dpad) ||
          (has_key_single(layout, dpad) && (stages == 1 || stages == 2));
@@ -417,6 +437,7 @@ int fgw_mha_plan(const fgw_mha_shape* s, const fgw_mha_request* req,
   const int wg_default = dev->wg_per_cu[layout] > 0 ? dev->wg_per_cu[layout] : 1;
 
   int splits = req->num_splits;
+  bool auto_single = false;  // automatic splits moved to the single-stage kernel
   if (splits != 0) {
     if (splits < 1 || splits > kMaxSplits || (splits & (splits - 1)))
       return fail(FGW_MHA_EINVAL, "num_splits supports None (automatic) or 1/2/4/.../%d",
@@ -453,6 +474,13 @@ int fgw_mha_plan(const fgw_mha_shape* s, const fgw_mha_request* req,
     while (splits < kAutoMaxSplits && tasks * splits * 2 <= slots &&
            (int64_t)(splits * 2) * min_keys <= capacity)
       splits *= 2;
+    if (req->stages == 0 && req->split_keys == 0) {
+      const int up = single_stage_splits(s, dev, layout, dpad, tasks, splits, capacity);
+      if (up > 0) {
+        splits = up;
+        auto_single = true;
+      }
+    }
   }
   const int64_t work = tasks * splits;
   if (work > INT32_MAX) return fail(FGW_MHA_EUNSUPPORTED, "work items exceed 2^31");
@@ -462,14 +490,14 @@ int fgw_mha_plan(const fgw_mha_shape* s, const fgw_mha_request* req,
                 "split_keys (length-balanced splits) needs the key layout, num_splits >= 2 and "
                 "B <= %d", kMaxBalancedBatch);
 
-  // Stages: the layout's default kernel unless the request names one. The key
-  // layout's single-stage kernel (head-dim tile 128, two workgroups per CU) is
-  // an explicit choice: measured faster only for long-cache decode split many
-  // ways (B2 H8 Q1 KV 32768: 64 splits on 512 programs 45.3 us against 47.1 us
-  // for 16 double-stage splits on 256), slower where a workgroup is alone on
-  // its CU (8 splits: 56.9 us against 47.7 us) and for large batches split a
+  // Stages: the layout's default kernel unless the request names one or the
+  // automatic splits moved to the key layout's single-stage kernel (head-dim
+  // tile 128, two workgroups per CU; single_stage_splits). Elsewhere that
+  // kernel measured slower: where a workgroup is alone on its CU (B2 H8
+  // KV 32768, 8 splits: 56.9 us against 47.7 us) and for large batches split a
   // few ways (B8 H32 KV 4096, 2 splits: 115.9 us against 101.7 us at 1 split).
-  const int stages = req->stages != 0 ? req->stages : default_stages(layout, dpad);
+  const int stages =
+      req->stages != 0 ? req->stages : (auto_single ? 1 : default_stages(layout, dpad));
   const int wg_kernel = stages == 1 && has_key_single(layout, dpad)
                             ? (dev->wg_per_cu_key_single > 0 ? dev->wg_per_cu_key_single : 1)
                             : wg_default;

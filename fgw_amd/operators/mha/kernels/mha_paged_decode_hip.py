@@ -301,6 +301,15 @@ def build_kernel(batch, sq, heads, dim, pool_rows, width, page_size, causal, dty
                                                                 width * page_size)
                 if balanced is not None:
                     splits, split_keys = balanced
+            if not split_keys and stages is None:
+                # The planner's automatic move to the single-stage key kernel,
+                # applied to the model's split count.
+                device = _device_info(device_index)
+                up = split_cost_model.single_stage_splits(
+                    batch, sq, heads, dim, width * page_size, splits, device.num_cus,
+                    device.wg_per_cu_key_single)
+                if up:
+                    splits, stages = up, 1
         else:
             splits = 0
         policy = split_policy

@@ -99,6 +99,26 @@ def planner_takes_prefill(batch, sq, heads, dim, num_cus, wg_per_cu, kv_tokens) 
             or batch * heads * sq * kv_tokens >= 1 << 24)
 
 
+def single_stage_splits(batch, sq, heads, dim, capacity_tokens, splits, num_cus,
+                        wg_per_cu_key_single) -> int:
+    """fgw_mha_plan's single_stage_splits (fmha_api.hip) restated: a short
+    decode plan (Sq <= 4, key layout, head-dim tile 128) of >= 16 even splits
+    that gives each CU at most one work item moves to the single-stage key
+    kernel with 4x the splits (>= 512 keys each), else 2x (>= 256 keys);
+    returns that split count, or 0 to keep the plan."""
+    dpad = 32
+    while dpad < dim:
+        dpad *= 2
+    if (dpad != 128 or sq > 4 or splits < 16 or wg_per_cu_key_single < 2
+            or batch * heads * splits > num_cus):
+        return 0
+    if 4 * splits <= SPLITS[-1] and capacity_tokens // (4 * splits) >= 512:
+        return 4 * splits
+    if 2 * splits <= SPLITS[-1] and capacity_tokens // (2 * splits) >= 256:
+        return 2 * splits
+    return 0
+
+
 def planner_fill_preferred(batch, sq, heads, kv_tokens) -> bool:
     """Query-layout shapes (Sq > 32) of at least 2^22 query-key pairs
     (B * H * Sq * table capacity), where fgw_mha_plan's own fill rule (four key

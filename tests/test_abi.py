@@ -60,6 +60,28 @@ def test_cost_model_guard_matches_the_planner_layout(lib):
                         assert (p.layout == 2) == want, (b, h, sq, d, kv)
 
 
+def test_single_stage_rule_matches_the_planner(lib):
+    # split_cost_model.single_stage_splits restates fgw_mha_plan's move of automatic
+    # short-decode plans to the single-stage key kernel (the Python host applies it
+    # to the cost model's split count).
+    from fgw_amd.operators.mha import split_cost_model as M
+    moved = 0
+    for b in (1, 2, 4, 16):
+        for h in (1, 4, 8, 32):
+            for sq in (1, 4, 5, 16):
+                for d in (64, 128):
+                    for kv in (1024, 4096, 8192, 32768, 65536):
+                        s = shape(b=b, h=h, sq=sq, d=d, kv=kv)
+                        fill = _lib.plan(s, _lib.Request(0, -1, -1, 0, 0 if d != 128 or sq > 32 else 2), DEVICE)
+                        auto = _lib.plan(s, _lib.Request(0, -1, -1), DEVICE)
+                        up = M.single_stage_splits(b, sq, h, d, kv, fill.num_splits, DEVICE.num_cus,
+                                                   DEVICE.wg_per_cu_key_single)
+                        want = (up, 1) if up else (fill.num_splits, fill.stages)
+                        assert (auto.num_splits, auto.stages) == want, (b, h, sq, d, kv)
+                        moved += bool(up)
+    assert moved >= 10
+
+
 def test_plan_headline_shapes(lib):
     # 2 x 8 x 16 prefill tiles of 256 rows fill the 256 CUs: prefill layout.
     prefill = _lib.plan(shape(sq=4096, kv=2048), _lib.Request(0, -1, -1), DEVICE)
@@ -92,10 +114,14 @@ def test_plan_headline_shapes(lib):
     assert (wide.layout, wide.dim_padded) == (0, 256)  # no prefill kernel for D > 128
     narrow = _lib.plan(shape(sq=4096, kv=2048, d=32), _lib.Request(0, -1, -1), DEVICE)
     assert narrow.layout == 0
+    # Decode: 16 double-stage splits fill the 256 CUs; the automatic plan moves to the
+    # single-stage key kernel with 4x the splits (512 keys each), two programs per CU.
     decode = _lib.plan(shape(sq=1, kv=32768), _lib.Request(0, -1, -1), DEVICE)
-    assert (decode.layout, decode.rows_per_tile, decode.num_splits, decode.work_items) == (1, 32, 16, 256)
-    assert (decode.stages, decode.grid) == (2, 256)
-    assert decode.parts_floats == 2 * 8 * 16 * 1 * 128 and decode.lse_floats == 2 * 8 * 16
+    assert (decode.layout, decode.rows_per_tile, decode.num_splits, decode.work_items) == (1, 32, 64, 1024)
+    assert (decode.stages, decode.grid) == (1, 512)
+    assert decode.parts_floats == 2 * 8 * 64 * 1 * 128 and decode.lse_floats == 2 * 8 * 64
+    fill = _lib.plan(shape(sq=1, kv=32768), _lib.Request(0, -1, -1, 0, 2), DEVICE)
+    assert (fill.num_splits, fill.stages, fill.grid) == (16, 2, 256)
     big = _lib.plan(shape(sq=32768, kv=2048), _lib.Request(0, -1, -1), DEVICE)
     assert big.layout == 2 and big.work_items == 2 * 8 * 128
     assert big.grid == 256  # persistent cap = 256 CUs x 1 program
@@ -162,7 +188,10 @@ def test_plan_kernel_stages(lib):
     assert (plan(shape(), 64, 1).stages, plan(shape(), 64, 1).grid) == (1, 512)
     assert (plan(shape(), 8, 1).stages, plan(shape(), 8, 1).grid) == (1, 128)
     assert (plan(shape(), 64, 2).stages, plan(shape(), 64, 2).grid) == (2, 256)
-    assert plan(shape(), 0, 1).num_splits == plan(shape()).num_splits  # splits do not move
+    # A requested stage count keeps the fill's split count; only the automatic plan
+    # moves to the single-stage kernel with more splits.
+    assert plan(shape(), 0, 1).num_splits == plan(shape(), 0, 2).num_splits == 16
+    assert (plan(shape()).num_splits, plan(shape()).stages) == (64, 1)
     # Other kernels have one stage count: accepted when requested, else refused.
     assert plan(shape(d=64)).stages == 2 and plan(shape(d=256)).stages == 1
     assert plan(shape(d=256), 0, 1).stages == 1

@@ -121,3 +121,16 @@ def test_balanced_split_keys():
     slots, keys = M.balanced_split_keys((0, 4096, 17, 1000, 2500), 4, 4096)
     assert sum(max(1, -(-n // keys)) for n in (0, 4096, 17, 1000, 2500)) <= 5 * 4
     assert 2 <= slots <= 128
+
+
+def test_single_stage_splits_known_answers():
+    # (batch, sq, heads, dim, capacity, splits) -> split count on the single-stage key
+    # kernel, 0 = keep the plan; 256 CUs, two single-stage programs per CU.
+    cases = [((2, 1, 8, 128, 32768, 16), 64), ((1, 1, 8, 128, 32768, 32), 64),
+             ((2, 1, 8, 128, 8192, 16), 32), ((2, 4, 8, 128, 65536, 16), 64),
+             ((2, 16, 8, 128, 32768, 16), 0), ((4, 1, 8, 128, 32768, 8), 0),
+             ((2, 1, 8, 64, 32768, 16), 0), ((4, 1, 8, 128, 32768, 16), 0),
+             ((1, 1, 1, 128, 4096, 64), 0), ((2, 1, 8, 128, 4096, 16), 0)]
+    for args, want in cases:
+        assert M.single_stage_splits(*args, 256, 2) == want, args
+    assert M.single_stage_splits(2, 1, 8, 128, 32768, 16, 256, 1) == 0
