@@ -86,7 +86,10 @@ typedef struct {
                                   ragged requests get work items of similar size. No reference
                                   counterpart (the reference splits every request evenly). */
   int32_t stages;              /* K/V stages per key group: 0 = the layout's default kernel
-                                  (double-stage for the key layout at head-dim tile 128);
+                                  (double-stage for the key layout at head-dim tile 128),
+                                  except that automatic short-decode plans (Sq <= 4, 16+
+                                  even splits, at most one work item per CU) move to the
+                                  single-stage kernel with 4x (or 2x) the splits;
                                   1 or 2 selects the key layout's single-stage (two
                                   workgroups per CU) or double-stage kernel where both exist
                                   (head-dim tile 128); elsewhere only the kernel's own count
@@ -158,7 +161,9 @@ int fgw_mha_query_device(int device, fgw_mha_device_info* info);
  * general_split_policy.py:9-21): automatic splits double while
  * B*H*q_tiles*(2 splits) still fits the device's resident workgroup slots
  * and every split keeps at least two rounds of key blocks (four in the
- * prefill layout). Stages: the layout's default kernel unless requested; the
+ * prefill layout, four in the query layout from 2^22 query-key pairs).
+ * Stages: the layout's default kernel unless requested or the automatic
+ * short-decode rule selects the key layout's single-stage kernel; the
  * persistent grid is capped at the selected kernel's resident slots. Errors
  * mirror the reference ValueErrors (v7.py:49-55, :97-99). */
 int fgw_mha_plan(const fgw_mha_shape* shape, const fgw_mha_request* request,
