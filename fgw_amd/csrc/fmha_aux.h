@@ -126,6 +126,43 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(MergeParams p, int
 // G group states are then rescaled to the common peak and summed in group
 // order through LDS, and O = acc / max(tot, 1e-30) is cast to the input
 // dtype. An all-empty row is exactly zero.
+// Group g's splits g, g + G, ... of a wide merge row (see merge_wide_kernel)
+// in chunks of CH whose loads are all issued before any is used; the running
+// peak moves once per chunk. Missing splits past `used` load split g again
+// and carry weight 0.
+template <int CH>
+__device__ __forceinline__ void wide_group(const float* ls, const float* ps, int64_t lse_stride,
+                                           int64_t part_stride, int g, int G, int used,
+                                           float& peak, float& tot, f32x4& acc) {
+  for (int s0 = g; s0 < used; s0 += CH * G) {
+    float x[CH];
+    f32x4 v[CH];
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int s = s0 + i * G < used ? s0 + i * G : g;  // clamped; weight 0 below
+      x[i] = ls[(int64_t)s * lse_stride];
+      v[i] = *reinterpret_cast<const f32x4*>(ps + (int64_t)s * part_stride);
+    }
+    float cpeak = peak;
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const bool live = s0 + i * G < used && x[i] > -1.0e29f;
+      cpeak = live ? fmaxf(cpeak, x[i]) : cpeak;
+    }
+    const float keep = expf(peak - cpeak);
+    tot *= keep;
+    acc *= keep;
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const bool live = s0 + i * G < used && x[i] > -1.0e29f;
+      const float wgt = live ? expf(x[i] - cpeak) : 0.0f;
+      tot += wgt;
+      acc += live ? v[i] * wgt : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    peak = cpeak;
+  }
+}
+
 template <bool BF16>
 __global__ __launch_bounds__(kMergeThreads) void merge_wide_kernel(MergeParams p) {
   using E = Elem<BF16>;
@@ -147,33 +184,16 @@ __global__ __launch_bounds__(kMergeThreads) void merge_wide_kernel(MergeParams p
   float peak = kNegBig, tot = 0.0f;
   f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
   if (act) {
-    for (int s0 = g; s0 < used; s0 += kMergeChunk * G) {
-      float x[kMergeChunk];
-      f32x4 v[kMergeChunk];
-#pragma unroll
-      for (int i = 0; i < kMergeChunk; ++i) {
-        const int s = s0 + i * G < used ? s0 + i * G : g;  // clamped; weight 0 below
-        x[i] = ls[(int64_t)s * p.sq];
-        v[i] = *reinterpret_cast<const f32x4*>(ps + (int64_t)s * part_stride);
-      }
-      float cpeak = peak;
-#pragma unroll
-      for (int i = 0; i < kMergeChunk; ++i) {
-        const bool live = s0 + i * G < used && x[i] > -1.0e29f;
-        cpeak = live ? fmaxf(cpeak, x[i]) : cpeak;
-      }
-      const float keep = expf(peak - cpeak);
-      tot *= keep;
-      acc *= keep;
-#pragma unroll
-      for (int i = 0; i < kMergeChunk; ++i) {
-        const bool live = s0 + i * G < used && x[i] > -1.0e29f;
-        const float wgt = live ? expf(x[i] - cpeak) : 0.0f;
-        tot += wgt;
-        acc += live ? v[i] * wgt : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      }
-      peak = cpeak;
-    }
+    // The smallest chunk of 4, 8 or 16 that holds a group's splits (16
+    // beyond): 64 splits over 8 groups are one chunk of 8, not 16 with half
+    // of the loads clamped. The live splits are summed in the same order.
+    const int per = (used + G - 1) / G;
+    if (per <= 4)
+      wide_group<4>(ls, ps, p.sq, part_stride, g, G, used, peak, tot, acc);
+    else if (per <= 8)
+      wide_group<8>(ls, ps, p.sq, part_stride, g, G, used, peak, tot, acc);
+    else
+      wide_group<kMergeChunk>(ls, ps, p.sq, part_stride, g, G, used, peak, tot, acc);
     if (c == 0) speak[g] = peak;  // the same in every thread of the group
   }
   __syncthreads();
