@@ -61,7 +61,11 @@ hipError_t launch_merge(bool bf16, const MergeParams& p, hipStream_t stream) {
     return hipGetLastError();
   }
   // One (row, 4 dims) pair per thread: a workgroup covers whole rows.
-  const int rows_per_wg = (4 * kMergeThreads) / p.dim > 0 ? (4 * kMergeThreads) / p.dim : 1;
+  int rows_per_wg = (4 * kMergeThreads) / p.dim > 0 ? (4 * kMergeThreads) / p.dim : 1;
+  // Tile-balanced plans merge a query tile's rows by its own slot count: a
+  // power-of-two row group never straddles two 256-row tiles.
+  if (p.rows_tile > 0)
+    while (rows_per_wg & (rows_per_wg - 1)) rows_per_wg &= rows_per_wg - 1;
   const int64_t groups = (p.sq + rows_per_wg - 1) / rows_per_wg;
   const dim3 grid((unsigned)((int64_t)p.batch * p.heads * groups));
   if (bf16) {
@@ -208,6 +212,29 @@ int rows_per_tile(int layout) {
 }
 // Head-dim tiles with a prefill-layout kernel.
 bool has_prefill(int dpad) { return dpad == 64 || dpad == 128; }
+
+// split_keys > 0 means length-balanced splits in the key layout and
+// tile-balanced causal splits in the prefill layout.
+bool tile_balanced(int layout, int causal, int split_keys) {
+  return split_keys > 0 && layout == kLayoutPrefill && causal;
+}
+bool split_keys_valid(const fgw_mha_shape* s, int layout, int splits, int split_keys) {
+  if (split_keys == 0) return true;
+  if (split_keys < 0 || splits < 2) return false;
+  return (layout == kLayoutKey && s->batch <= kMaxBalancedBatch) ||
+         tile_balanced(layout, s->causal, split_keys);
+}
+// Work items of a tile-balanced causal plan: every (b, h) takes
+// tile_slots(t) items of each 256-row query tile t.
+int64_t tile_balanced_work(const fgw_mha_shape* s, int splits, int split_keys) {
+  const int rows = 256;
+  const int q_tiles = (s->sq + rows - 1) / rows;
+  const int capacity = s->width * s->page_size;
+  int64_t per_bh = 0;
+  for (int t = 0; t < q_tiles; ++t)
+    per_bh += tile_slots(t, s->sq, capacity, rows, split_keys, splits);
+  return (int64_t)s->batch * s->heads * per_bh;
+}
 // The automatic layout choice takes the prefill layout for Q longer than one
 // query-layout tile (Sq > 128) when its 256-row query tiles alone give every
 // resident program of the device a work item, when Sq >= 1024, or when the
@@ -270,13 +297,14 @@ int check_plan(const fgw_mha_shape* s, const fgw_mha_plan_t* p) {
   const int rows = rows_per_tile(p->layout);
   const int q_tiles = (s->sq + rows - 1) / rows;
   const int64_t tasks = (int64_t)s->batch * s->heads * q_tiles;
+  const int64_t work = tile_balanced(p->layout, s->causal, p->split_keys)
+                           ? tile_balanced_work(s, p->num_splits, p->split_keys)
+                           : tasks * p->num_splits;
   if (p->rows_per_tile != rows || p->q_tiles != q_tiles || p->query_tile_tasks != tasks ||
-      p->num_splits < 1 || p->num_splits > kMaxSplits ||
-      p->work_items != tasks * p->num_splits || p->grid < 1 || p->grid > p->work_items ||
+      p->num_splits < 1 || p->num_splits > kMaxSplits || p->work_items != work ||
+      p->grid < 1 || p->grid > p->work_items ||
       p->dim_padded != dim_tile(s->dim) || p->execution_mode != (p->num_splits > 1 ? 1 : 0) ||
-      p->split_keys < 0 ||
-      (p->split_keys > 0 && (p->layout != kLayoutKey || p->num_splits < 2 ||
-                             s->batch > kMaxBalancedBatch)) ||
+      !split_keys_valid(s, p->layout, p->num_splits, p->split_keys) ||
       !stages_valid(p->layout, p->dim_padded, p->stages))
     return fail(FGW_MHA_EINVAL, "plan does not match the shape; call fgw_mha_plan");
   return FGW_MHA_OK;
@@ -321,6 +349,7 @@ FwdParams make_params(const fgw_mha_shape* s, const fgw_mha_plan_t* p, const fgw
   f.work = p->work_items;
   f.mode = mode;
   f.split_keys = mode == 1 ? p->split_keys : 0;
+  f.split_direct = 0;
   page_divisor((uint32_t)s->page_size, &f.page_magic, &f.page_shift);
   f.scale_log2 = (float)(1.4426950408889634 / __builtin_sqrt((double)s->dim));
   f.segs = nullptr;
@@ -349,18 +378,22 @@ int check_schedule(const fgw_mha_shape* s, const fgw_mha_schedule* sc) {
   return FGW_MHA_OK;
 }
 
+// `whole`: the partial kernel of a full call, whose merge follows (a
+// tile-balanced plan's one-split tiles then write their output directly).
 int launch_partial_kernel(const fgw_mha_shape* s, const fgw_mha_plan_t* p,
-                          const fgw_mha_tensors* t, int mode, hipStream_t stream) {
+                          const fgw_mha_tensors* t, int mode, hipStream_t stream,
+                          bool whole = false) {
   const int stages = p->stages == default_stages(p->layout, p->dim_padded) ? 0 : p->stages;
   const FwdEntry e = fwd_entry(s->dtype == FGW_MHA_BFLOAT16, p->dim_padded, p->layout, stages);
   if (!e.launch) return fail(FGW_MHA_EUNSUPPORTED, "no kernel for dim tile %d", p->dim_padded);
-  const FwdParams f = make_params(s, p, t, mode);
+  FwdParams f = make_params(s, p, t, mode);
+  f.split_direct = whole && mode == 1 && tile_balanced(p->layout, s->causal, p->split_keys);
   const hipError_t err = e.launch(f, p->grid, stream);
   return err == hipSuccess ? FGW_MHA_OK : hip_fail(err, "forward kernel launch");
 }
 
 int launch_merge_kernel(const fgw_mha_shape* s, const fgw_mha_plan_t* p, const fgw_mha_tensors* t,
-                        hipStream_t stream) {
+                        hipStream_t stream, bool whole = false) {
   MergeParams m;
   m.parts = t->parts;
   m.lse = t->lse;
@@ -373,6 +406,8 @@ int launch_merge_kernel(const fgw_mha_shape* s, const fgw_mha_plan_t* p, const f
   m.lengths = t->cache_seqlens;
   m.split_keys = p->split_keys;
   m.capacity = s->width * s->page_size;
+  m.rows_tile = tile_balanced(p->layout, s->causal, p->split_keys) ? 256 : 0;
+  m.skip_single = whole && m.rows_tile > 0;
   const hipError_t err = launch_merge(s->dtype == FGW_MHA_BFLOAT16, m, stream);
   return err == hipSuccess ? FGW_MHA_OK : hip_fail(err, "merge kernel launch");
 }
@@ -482,13 +517,16 @@ int fgw_mha_plan(const fgw_mha_shape* s, const fgw_mha_request* req,
       }
     }
   }
-  const int64_t work = tasks * splits;
-  if (work > INT32_MAX) return fail(FGW_MHA_EUNSUPPORTED, "work items exceed 2^31");
   if (req->split_keys < 0) return fail(FGW_MHA_EINVAL, "split_keys must be 0 or positive");
-  if (req->split_keys > 0 && (layout != kLayoutKey || splits < 2 || s->batch > kMaxBalancedBatch))
+  if (!split_keys_valid(s, layout, splits, req->split_keys))
     return fail(FGW_MHA_EINVAL,
-                "split_keys (length-balanced splits) needs the key layout, num_splits >= 2 and "
-                "B <= %d", kMaxBalancedBatch);
+                "split_keys needs num_splits >= 2 and either the key layout with B <= %d "
+                "(length-balanced splits) or the causal prefill layout (tile-balanced splits)",
+                kMaxBalancedBatch);
+  const int64_t work = tile_balanced(layout, s->causal, req->split_keys)
+                           ? tile_balanced_work(s, splits, req->split_keys)
+                           : tasks * splits;
+  if (work > INT32_MAX) return fail(FGW_MHA_EUNSUPPORTED, "work items exceed 2^31");
 
   // Stages: the layout's default kernel unless the request names one or the
   // automatic splits moved to the key layout's single-stage kernel (head-dim
@@ -541,9 +579,9 @@ int fgw_mha_fwd(const fgw_mha_shape* s, const fgw_mha_plan_t* p, const fgw_mha_t
   if (!rc) rc = check_tensors(t, true, true, p->num_splits > 1);
   if (rc) return rc;
   if (p->num_splits == 1) return launch_partial_kernel(s, p, t, 0, stream);
-  rc = launch_partial_kernel(s, p, t, 1, stream);
+  rc = launch_partial_kernel(s, p, t, 1, stream, true);
   if (rc) return rc;
-  return launch_merge_kernel(s, p, t, stream);
+  return launch_merge_kernel(s, p, t, stream, true);
 }
 
 int fgw_mha_fwd_noalloc(const fgw_mha_shape* s, const fgw_mha_plan_t* p,
@@ -568,9 +606,9 @@ int fgw_mha_fwd_noalloc(const fgw_mha_shape* s, const fgw_mha_plan_t* p,
   fgw_mha_tensors w = *t;
   w.parts = base;  // 256-byte aligned
   w.lse = base + p->parts_floats;
-  rc = launch_partial_kernel(s, p, &w, 1, stream);
+  rc = launch_partial_kernel(s, p, &w, 1, stream, true);
   if (rc) return rc;
-  return launch_merge_kernel(s, p, &w, stream);
+  return launch_merge_kernel(s, p, &w, stream, true);
 }
 
 int fgw_mha_partial(const fgw_mha_shape* s, const fgw_mha_plan_t* p, const fgw_mha_tensors* t,
@@ -587,7 +625,7 @@ int fgw_mha_merge(const fgw_mha_shape* s, const fgw_mha_plan_t* p, const fgw_mha
   int rc = check_shape(s);
   if (!rc) rc = check_plan(s, p);
   if (!rc) rc = check_tensors(t, false, true, true);
-  if (!rc && p->split_keys > 0 && !t->cache_seqlens)
+  if (!rc && p->split_keys > 0 && p->layout == kLayoutKey && !t->cache_seqlens)
     rc = fail(FGW_MHA_EINVAL, "a length-balanced plan merges by cache_seqlens; it is NULL");
   if (rc) return rc;
   return launch_merge_kernel(s, p, t, stream);

@@ -78,10 +78,13 @@ __device__ __forceinline__ void merge_one(const float* ls, int64_t lse_stride, c
     merge_one_chunked<BF16, kMergeChunk>(ls, lse_stride, ps, part_stride, splits, dst);
 }
 
-// Splits row (b, ., .) of a merge reads: all slots, or the balanced count
-// of request b (balanced_splits over its clamped length).
-__device__ __forceinline__ int merge_splits(const MergeParams& p, int b) {
+// Splits row (b, ., q) of a merge reads: all slots, the balanced count of
+// request b (balanced_splits over its clamped length), or the slots of q's
+// query tile in a tile-balanced causal plan.
+__device__ __forceinline__ int merge_splits(const MergeParams& p, int b, int q) {
   if (p.split_keys <= 0) return p.splits;
+  if (p.rows_tile > 0)
+    return tile_slots(q / p.rows_tile, p.sq, p.capacity, p.rows_tile, p.split_keys, p.splits);
   int len = p.lengths[b];
   len = len < 0 ? 0 : (len > p.capacity ? p.capacity : len);
   return balanced_splits(len, p.split_keys, p.splits);
@@ -113,7 +116,9 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(MergeParams p, int
   const int q0 = g * rows_per_wg;
   const int rows = p.sq - q0 < rows_per_wg ? p.sq - q0 : rows_per_wg;
   const int b = bh / p.heads;
-  merge_rows<BF16>(p.parts, p.lse, p.out, p.sq, p.heads, p.dim, p.splits, merge_splits(p, b), b,
+  const int used = merge_splits(p, b, q0);
+  if (p.skip_single && used == 1) return;  // written by the forward kernel
+  merge_rows<BF16>(p.parts, p.lse, p.out, p.sq, p.heads, p.dim, p.splits, used, b,
                    bh % p.heads, q0, rows, threadIdx.x, kMergeThreads);
 }
 
@@ -180,7 +185,8 @@ __global__ __launch_bounds__(kMergeThreads) void merge_wide_kernel(MergeParams p
   const float* ls = p.lse + base;
   const float* ps = p.parts + base * p.dim + 4 * c;
   const int64_t part_stride = (int64_t)p.sq * p.dim;
-  const int used = merge_splits(p, b);
+  const int used = merge_splits(p, b, q);
+  if (p.skip_single && used == 1) return;  // written by the forward kernel (whole workgroup)
   float peak = kNegBig, tot = 0.0f;
   f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
   if (act) {

@@ -549,12 +549,13 @@ __device__ __forceinline__ void pv_block(const unsigned char* vt, const Lanes<C>
 template <class C>
 __device__ __forceinline__ void store_row(const FwdParams& p, int b, int h, int split, int qrow,
                                           int d0, f32x4 val, float inv, int slot = -1,
-                                          int q0 = 0) {
+                                          int q0 = 0, int mode = -1) {
   using E = Elem<C::BF16>;
-  if (p.mode == 2 && slot >= 0) {
+  if (mode < 0) mode = p.mode;
+  if (mode == 2 && slot >= 0) {
     float* dst = p.parts + ((int64_t)slot * C::ROWS_TILE + (qrow - q0)) * p.dim + d0;
     *reinterpret_cast<f32x4*>(dst) = val * inv;
-  } else if (p.mode != 1) {
+  } else if (mode != 1) {
     u16* dst = static_cast<u16*>(p.out) + (((int64_t)b * p.sq + qrow) * p.heads + h) * p.dim + d0;
     u32x2 w;
     w.x = E::pack2(val[0] * inv, val[1] * inv);
@@ -651,6 +652,20 @@ __device__ __forceinline__ int split_bound(int nblk, int s, int splits) {
 
 // Splits of a request of len live keys in a length-balanced plan: enough
 // that none holds more than split_keys keys, at least 1, at most splits.
+// Tile-balanced causal splits (prefill layout, causal, split_keys > 0): the
+// key slots of query tile t are its visible keys at full table capacity
+// split_keys per slot, at least one and at most `splits`, so that a long tile
+// of a causal prefill is cut into work items of similar size while the short
+// ones stay whole. Shared by the planner, the kernel and the merge.
+__host__ __device__ __forceinline__ int tile_slots(int t, int sq, int capacity, int rows_tile,
+                                                   int split_keys, int splits) {
+  const int end = (t + 1) * rows_tile < sq ? (t + 1) * rows_tile : sq;
+  int vis = capacity - sq + end;
+  vis = vis < 0 ? 0 : (vis > capacity ? capacity : vis);
+  const int n = vis > 0 ? (vis - 1) / split_keys + 1 : 1;
+  return n < splits ? n : splits;
+}
+
 __device__ __forceinline__ int balanced_splits(int len, int split_keys, int splits) {
   const int s = len > 0 ? (len - 1) / split_keys + 1 : 1;
   return s < splits ? s : splits;

@@ -42,8 +42,13 @@ struct FwdParams {
   int32_t slots;
   int32_t seg_scale;  // kernel key blocks per schedule key block
   // Length-balanced splits (key layout, mode 1): request b takes
-  // balanced_splits(len_b, split_keys, splits) splits; 0 = even splits.
+  // balanced_splits(len_b, split_keys, splits) splits; tile-balanced causal
+  // splits (prefill layout, causal, mode 1): query tile t takes
+  // tile_slots(t, ...) splits; 0 = even splits.
   int32_t split_keys;
+  // Tile-balanced plans in a whole call: a tile of one split writes its
+  // normalised output rows directly (the merge skips them).
+  int32_t split_direct;
 };
 
 struct MergeParams {
@@ -53,8 +58,12 @@ struct MergeParams {
   int32_t batch, sq, heads, dim, splits;
   // Length-balanced splits: row (b, ., .) merges the first
   // balanced_splits(len_b, split_keys, splits) slots; 0 = all slots.
-  const int32_t* lengths;  // [B], read only when split_keys > 0
+  const int32_t* lengths;  // [B], read only when split_keys > 0 and rows_tile == 0
   int32_t split_keys, capacity;
+  // Tile-balanced causal splits: rows of query tile t merge the first
+  // tile_slots(t, ...) slots; rows per query tile, 0 = not such a plan.
+  int32_t rows_tile;
+  int32_t skip_single;  // 1: rows of one-slot tiles were written directly; skip them
 };
 
 // Merge of the static schedule's split tiles: group g = (task, first slot,

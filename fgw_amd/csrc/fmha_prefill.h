@@ -299,14 +299,37 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p,
 
   for (int it = 0; it < count; ++it) {
     int w = first + it;
-    const int split = w % p.splits;
-    w /= p.splits;
-    // Causal tiles: the last (heaviest) first, so that a dispatcher or a
-    // persistent program starts the long work items early.
-    const int qt = p.causal ? p.q_tiles - 1 - w % p.q_tiles : w % p.q_tiles;
-    w /= p.q_tiles;
-    const int h = w % p.heads;
-    const int b = w / p.heads;
+    int split, nsplit = p.splits, qt, h, b;
+    if (p.split_keys > 0) {
+      // Tile-balanced causal plan: the items of one (b, h) are contiguous
+      // (a program's range, and with the XCD remap one XCD's, shares its K/V
+      // in L2), its tiles from the last (heaviest) one, tile t in
+      // tile_slots(t) splits.
+      int per_bh = 0;
+      for (int t = 0; t < p.q_tiles; ++t)
+        per_bh += tile_slots(t, p.sq, capacity, C::ROWS_TILE, p.split_keys, p.splits);
+      const int bh = w / per_bh;
+      int r = w - bh * per_bh, t = p.q_tiles - 1, n = 1;
+      for (;; --t) {
+        n = tile_slots(t, p.sq, capacity, C::ROWS_TILE, p.split_keys, p.splits);
+        if (r < n || t == 0) break;
+        r -= n;
+      }
+      split = r;
+      nsplit = n;
+      qt = t;
+      h = bh % p.heads;
+      b = bh / p.heads;
+    } else {
+      split = w % p.splits;
+      w /= p.splits;
+      // Causal tiles: the last (heaviest) first, so that a dispatcher or a
+      // persistent program starts the long work items early.
+      qt = p.causal ? p.q_tiles - 1 - w % p.q_tiles : w % p.q_tiles;
+      w /= p.q_tiles;
+      h = w % p.heads;
+      b = w / p.heads;
+    }
     const int32_t* table_b = table + (int64_t)b * p.width;
     const char* kb = static_cast<const char*>(p.k) + (int64_t)h * p.dim * 2;
     const char* vb = static_cast<const char*>(p.v) + (int64_t)h * p.dim * 2;
@@ -318,8 +341,8 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p,
     int max_vis = p.causal ? len - p.sq + tile_last + 1 : len;
     max_vis = max_vis < 0 ? 0 : (max_vis > len ? len : max_vis);
     const int nblk = (max_vis + C::BN - 1) / C::BN;
-    const int blk_begin = (int)((int64_t)nblk * split / p.splits);
-    const int blk_end = (int)((int64_t)nblk * (split + 1) / p.splits);
+    const int blk_begin = (int)((int64_t)nblk * split / nsplit);
+    const int blk_end = (int)((int64_t)nblk * (split + 1) / nsplit);
     const int N = blk_end - blk_begin;
     const int key0 = blk_begin * C::BN;
 
@@ -463,12 +486,15 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p,
     }
 
     const float tot = pair_sum(l);
+    // Partials, unless a one-split tile of a tile-balanced whole call writes
+    // its output rows directly.
+    const bool to_parts = p.mode == 1 && !(p.split_direct && nsplit == 1);
     if (p.dim == C::DPAD) {
       // Every wave's DMA into the rings has landed (each waited for its own
       // above) and no wave reads them any more: the rings stage the output.
       __syncthreads();
       static_assert(C::WAVES * 32 * kStagedRowBytes<C> <= C::LDS_BYTES, "staged rows fit the rings");
-      const bool f32 = p.mode == 1;
+      const bool f32 = to_parts;
       float* fdst =
           f32 ? p.parts + ((((int64_t)b * p.heads + h) * p.splits + split) * p.sq + row_base) *
                               C::DPAD
@@ -479,7 +505,7 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p,
       store_rows_staged<C>(smem + wave * 32 * kStagedRowBytes<C>, lane, o,
                            1.0f / fmaxf(tot, 1.0e-30f), f32, fdst, bdst,
                            (int64_t)p.heads * C::DPAD * 2, p.sq - row_base);
-      if (p.mode == 1 && hh == 0 && qrow < p.sq)
+      if (to_parts && hh == 0 && qrow < p.sq)
         p.lse[(((int64_t)b * p.heads + h) * p.splits + split) * p.sq + qrow] = lse_of(m, tot);
     } else if (qrow < p.sq) {
       const float inv = 1.0f / fmaxf(tot, 1.0e-30f);
@@ -490,10 +516,10 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p,
           const int d0 = 32 * dt + 8 * gq + 4 * hh;
           if (d0 < p.dim) {
             f32x4 val = {o[dt][4 * gq], o[dt][4 * gq + 1], o[dt][4 * gq + 2], o[dt][4 * gq + 3]};
-            store_row<C>(p, b, h, split, qrow, d0, val, inv);
+            store_row<C>(p, b, h, split, qrow, d0, val, inv, -1, 0, to_parts ? 1 : 0);
           }
         }
-      if (p.mode == 1 && hh == 0) {
+      if (to_parts && hh == 0) {
         p.lse[(((int64_t)b * p.heads + h) * p.splits + split) * p.sq + qrow] = lse_of(m, tot);
       }
     }

@@ -114,10 +114,14 @@ class _Launch(_launch.Launcher):
         self.requested_split_policy = meta["requested_split_policy"]
         self.split_policy = meta["split_policy"]
         self.num_splits = plan.num_splits
-        # Length-balanced splits: request b takes clamp(ceil(len_b / split_keys),
-        # 1, num_splits) of the num_splits slots; 0 = every request num_splits.
+        # split_keys > 0: length-balanced splits in the key layout (request b
+        # takes clamp(ceil(len_b / split_keys), 1, num_splits) of the slots),
+        # tile-balanced causal splits in the prefill layout (query tile t takes
+        # clamp(ceil(visible keys at capacity / split_keys), 1, num_splits));
+        # 0 = every task num_splits.
         self.split_keys = plan.split_keys
-        self.split_balance = "length" if plan.split_keys else "even"
+        self.split_balance = ("tile" if plan.layout == _LAYOUTS["prefill"] else "length") \
+            if plan.split_keys else "even"
         self.query_tile_tasks = plan.query_tile_tasks
         self.execution_mode = "split_and_merge" if plan.execution_mode else "direct_single_split"
         self.execution_path = ROUTE
@@ -184,9 +188,10 @@ class _Launch(_launch.Launcher):
                 lse.view(s.batch, s.heads, self.num_splits, s.sq))
 
     def _merge(self, parts, lse, cache_seqlens=None):
-        """Output from the partials. A length-balanced plan (split_keys > 0)
-        merges request b's first clamp(ceil(len_b / split_keys), 1, S) slots
-        and needs the call's cache_seqlens."""
+        """Output from the partials. A length-balanced plan (key layout,
+        split_keys > 0) merges request b's first clamp(ceil(len_b /
+        split_keys), 1, S) slots and needs the call's cache_seqlens; a
+        tile-balanced plan merges each query tile's own slot count."""
         s = self._shape
         if (parts.dtype != torch.float32 or lse.dtype != torch.float32
                 or parts.numel() != self._plan.parts_floats or lse.numel() != self._plan.lse_floats
@@ -197,7 +202,7 @@ class _Launch(_launch.Launcher):
                                           or tuple(cache_seqlens.shape) != self._meta_shapes[1]
                                           or cache_seqlens.device != self._device):
             raise ValueError("cache_seqlens must be this kernel's int32 [B] lengths on its GPU")
-        if self.split_keys and cache_seqlens is None:
+        if self.split_balance == "length" and cache_seqlens is None:
             raise ValueError("a length-balanced plan merges by cache_seqlens")
         out = torch.empty(self._out_shape, dtype=self._dtype, device=self._device)
         t = _lib.Tensors(None, None, None, None,

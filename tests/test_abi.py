@@ -309,3 +309,26 @@ def test_launch_shim_loads_and_checks_its_arguments(lib):
         call(q, kv, kv, table.long(), lengths)
     with pytest.raises(ValueError, match="same GPU"):  # CPU tensors
         call(q, kv, kv, table, lengths)
+
+
+def test_plan_tile_balanced_causal_splits(lib):
+    # Prefill layout, causal: split_keys gives each 256-row query tile
+    # clamp(ceil(visible keys at capacity / split_keys), 1, num_splits) work items.
+    s = shape(b=2, h=8, sq=4096, kv=4096, causal=1)
+    p = _lib.plan(s, _lib.Request(2, -1, 2, 2176), DEVICE)
+    # tiles 0-7 see 256..2048 keys (one slot), tiles 8-15 see 2304..4096 (two)
+    assert (p.layout, p.num_splits, p.split_keys, p.work_items) == (2, 2, 2176, 16 * (8 + 16))
+    assert p.grid == p.work_items  # causal plans stay uncapped
+    capped = _lib.plan(s, _lib.Request(2, 64, 2, 2176), DEVICE)
+    assert capped.grid == 64 and capped.work_items == 384
+    wide = _lib.plan(s, _lib.Request(32, -1, 2, 256), DEVICE)
+    assert wide.work_items == 16 * sum(min(32, -(-256 * (t + 1) // 256)) for t in range(16))
+    ragged = _lib.plan(shape(b=1, h=2, sq=300, kv=1000, causal=1), _lib.Request(4, -1, 2, 256),
+                       DEVICE)
+    # capacity 1024, Sq 300: tile 0 sees up to 980 keys (4 slots), tile 1 all 1024 (4)
+    assert ragged.work_items == 2 * (4 + 4)
+    for req, shp in ((_lib.Request(2, -1, 2, 256), shape(sq=4096, kv=4096)),  # not causal
+                     (_lib.Request(1, -1, 2, 256), s),  # one split
+                     (_lib.Request(2, -1, 0, 256), s)):  # query layout
+        with pytest.raises(ValueError, match="split_keys"):
+            _lib.plan(shp, req, DEVICE)
