@@ -332,3 +332,20 @@ def test_plan_tile_balanced_causal_splits(lib):
                      (_lib.Request(2, -1, 0, 256), s)):  # query layout
         with pytest.raises(ValueError, match="split_keys"):
             _lib.plan(shp, req, DEVICE)
+
+
+def test_plan_automatic_tile_balanced_causal_splits(lib):
+    # Causal self-attention with at most half the device's programs in query tiles
+    # of very different lengths: the planner cuts the long tiles.
+    auto = _lib.plan(shape(b=1, h=8, sq=4096, kv=4096, causal=1), _lib.Request(0, -1, -1), DEVICE)
+    # 1.5 x 278528 keys / 256 CUs = 1632 -> 1664 keys per item; the longest tile takes 3
+    assert (auto.layout, auto.num_splits, auto.split_keys) == (2, 4, 1664)
+    assert auto.work_items == 8 * sum(-(-256 * (t + 1) // 1664) for t in range(16))
+    # Left alone: a prefix-cached shape (tiles of similar lengths), short tiles, and
+    # as many tiles as half the programs and more.
+    for s in (shape(b=1, h=8, sq=1024, kv=8192, causal=1), shape(b=1, h=32, sq=1024, kv=1024, causal=1),
+              shape(b=1, h=16, sq=4096, kv=4096, causal=1), shape(b=1, h=8, sq=4096, kv=4096)):
+        assert _lib.plan(s, _lib.Request(0, -1, -1), DEVICE).split_keys == 0
+    # An explicit split count keeps even splits.
+    assert _lib.plan(shape(b=1, h=8, sq=4096, kv=4096, causal=1), _lib.Request(2, -1, -1),
+                     DEVICE).split_keys == 0

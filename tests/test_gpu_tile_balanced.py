@@ -62,3 +62,22 @@ def test_tile_balanced_components_equal_the_full_call():
     assert torch.equal(full, merged)
     check_output(full.cpu(), O.chunked_reference(q, k, v, table, lengths, page, True, 128), q,
                  lengths, True, "tile-balanced components")
+
+
+def test_automatic_tile_balanced_plan():
+    # Causal self-attention in 64 query tiles of 256..4096 visible keys: the planner
+    # picks a tile-balanced plan by itself.
+    from fgw_amd.operators.mha.current import build_kernel
+    b, sq, h, dim, page = 1, 4096, 4, 128, 128
+    width = sq // page
+    case = ("tiles_auto", b, sq, h, dim, page, width)
+    q, k, v, table = O.make_inputs(case, 13, torch.bfloat16)
+    lengths = torch.tensor([sq], dtype=torch.int32)
+    kern = build_kernel(b, sq, h, dim, k.shape[0], width, page, True, "bfloat16", 0,
+                        full_kv_cache=True)
+    assert kern.layout == "prefill" and kern.split_balance == "tile" and kern.split_keys > 0
+    got = kern(*(x.cuda() for x in (q, k, v, table, lengths)))
+    torch.cuda.synchronize()
+    check_output(got.cpu(), O.chunked_reference(q, k, v, table, lengths, page, True, 128), q,
+                 lengths, True, f"automatic tile-balanced plan splits={kern.num_splits} "
+                                f"split_keys={kern.split_keys}")
