@@ -83,8 +83,14 @@ typedef struct {
                                   splits balanced by length (key layout, num_splits > 1, B <=
                                   FGW_MHA_MAX_BALANCED_BATCH): request b takes
                                   clamp(ceil(len_b / split_keys), 1, num_splits) splits, so
-                                  ragged requests get work items of similar size. No reference
-                                  counterpart (the reference splits every request evenly). */
+                                  ragged requests get work items of similar size; in the
+                                  causal prefill layout (num_splits > 1), tile-balanced
+                                  splits: query tile t takes clamp(ceil(its visible keys at
+                                  table capacity / split_keys), 1, num_splits) work items
+                                  (fgw_mha_plan may choose these itself for causal plans
+                                  with few tiles of very different lengths and reports them
+                                  in fgw_mha_plan_t.split_keys). No reference counterpart
+                                  (the reference splits every request evenly). */
   int32_t stages;              /* K/V stages per key group: 0 = the layout's default kernel
                                   (double-stage for the key layout at head-dim tile 128),
                                   except that automatic short-decode plans (Sq <= 4, 16+
