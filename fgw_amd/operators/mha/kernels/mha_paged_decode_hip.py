@@ -241,14 +241,17 @@ def build_kernel(batch, sq, heads, dim, pool_rows, width, page_size, causal, dty
     cube_general.py:17, :45) and layout ("query" = 4 waves split 128 query
     rows; "prefill" = 8 waves split 256 query rows in two groups that
     alternate matrix and softmax phases, D in (32, 128]; "key" = waves split
-    key blocks; None: key for Sq <= 32; prefill when its 256-row tiles fill
-    the device, or, with KV splits, from Sq 1024, for D in (32, 128]; else
-    query), split_keys (extra; with an explicit num_splits >= 2 and the key
-    layout: request b takes clamp(ceil(len_b / split_keys), 1, num_splits)
-    splits; the automatic split chooses it itself for ragged host-known
-    lengths) and stages (extra; K/V stages per key group: None = the
-    layout's default kernel, 1 or 2 = the key layout's single- or
-    double-stage kernel at head-dim tile 128). The reference caches build_kernel on its
+    key blocks; None: key for Sq <= 32; for D in (32, 128] and Sq > 128,
+    prefill when its 256-row tiles fill the device, from Sq 1024, or from
+    2^24 query-key pairs; else query), split_keys (extra; with an explicit
+    num_splits >= 2: in the key layout request b takes clamp(ceil(len_b /
+    split_keys), 1, num_splits) splits, in the causal prefill layout query
+    tile t takes clamp(ceil(its visible keys at capacity / split_keys), 1,
+    num_splits); the automatic split chooses the first for ragged host-known
+    decode lengths and the second for causal plans with few tiles of very
+    different lengths) and stages (extra; K/V stages per key group: None =
+    the planner's choice, 1 or 2 = the key layout's single- or double-stage
+    kernel at head-dim tile 128). The reference caches build_kernel on its
     static arguments (lru_cache(128), v7.py:32); here the split count is
     chosen first (the cost model reads cache_lengths only under the
     auto/cost_model policy) and the plans are cached per (shape, split count,
