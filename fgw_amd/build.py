@@ -67,6 +67,9 @@ def _build_shim() -> pathlib.Path:
     tmp = out.with_name(out.name + ".tmp")
     cmd = ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wno-unused-function",
            "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
+           # The C++ ABI torch itself was built with (torch.utils.cpp_extension
+           # passes the same define).
+           f"-D_GLIBCXX_USE_CXX11_ABI={int(torch._C._GLIBCXX_USE_CXX11_ABI)}",
            f"-I{tdir / 'include'}", f"-I{tdir / 'include' / 'torch' / 'csrc' / 'api' / 'include'}",
            "-I/opt/rocm/include", f"-I{sysconfig.get_paths()['include']}",
            str(SHIM_SOURCE), "-o", str(tmp), f"-L{tdir / 'lib'}", f"-Wl,-rpath,{tdir / 'lib'}",

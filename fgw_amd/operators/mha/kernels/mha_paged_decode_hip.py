@@ -200,8 +200,9 @@ class _Launch(_launch.Launcher):
             raise ValueError("merge expects this kernel's contiguous fp32 partials and LSE")
         if cache_seqlens is not None and (cache_seqlens.dtype != torch.int32
                                           or tuple(cache_seqlens.shape) != self._meta_shapes[1]
-                                          or cache_seqlens.device != self._device):
-            raise ValueError("cache_seqlens must be this kernel's int32 [B] lengths on its GPU")
+                                          or cache_seqlens.device != self._device
+                                          or not cache_seqlens.is_contiguous()):
+            raise ValueError("cache_seqlens must be this kernel's contiguous int32 [B] lengths on its GPU")
         if self.split_balance == "length" and cache_seqlens is None:
             raise ValueError("a length-balanced plan merges by cache_seqlens")
         out = torch.empty(self._out_shape, dtype=self._dtype, device=self._device)
@@ -309,9 +310,10 @@ def build_kernel(batch, sq, heads, dim, pool_rows, width, page_size, causal, dty
                                                                 width * page_size)
                 if balanced is not None:
                     splits, split_keys = balanced
-            if not split_keys and stages is None:
+            if not split_keys and stages is None and layout in (None, "key"):
                 # The planner's automatic move to the single-stage key kernel,
-                # applied to the model's split count.
+                # applied to the model's split count (the single-stage kernel
+                # exists in the key layout only).
                 device = _device_info(device_index)
                 up = split_cost_model.single_stage_splits(
                     batch, sq, heads, dim, width * page_size, splits, device.num_cus,
@@ -356,14 +358,24 @@ def mha_paged_decode(q, k_cache, v_cache, block_table, cache_seqlens, page_size,
     if any(n < 0 or n > capacity for n in lengths):
         raise ValueError("Cache lengths must be within table capacity")
     full_kv_cache = all(n == capacity for n in lengths)
-    # Ragged lengths matter only to the cost model (v7_experimental.py:878-883
-    # forwards them only under that policy); other calls plan without them.
-    wants_lengths = (not full_kv_cache and num_splits is None
-                     and split_policy in ("auto", "cost_model") and not is_causal)
     with torch.cuda.device(q.device):
         kernel = build_kernel(b, sq, h, d, k_cache.shape[0], block_table.shape[1], page_size,
                               bool(is_causal), "float16" if q.dtype == torch.float16 else "bfloat16",
                               q.device.index, num_splits=num_splits, split_policy=split_policy,
                               full_kv_cache=full_kv_cache, persistent_programs=persistent_programs,
-                              cache_lengths=tuple(lengths) if wants_lengths else None)
+                              cache_lengths=planning_lengths(lengths, full_kv_cache, num_splits,
+                                                             split_policy, is_causal))
         return kernel(*inputs)
+
+
+def planning_lengths(lengths, full_kv_cache, num_splits, split_policy, is_causal):
+    """The host lengths mha_paged_decode hands to build_kernel, or None.
+
+    Ragged lengths matter only to the cost model: an explicit cost_model
+    request always receives them (v7_experimental.py:885-886, causal or not);
+    under 'auto' only non-causal calls, the ones the model's calibrated scope
+    admits, plan with them. Full caches and explicit split counts plan without
+    them."""
+    wants = (not full_kv_cache and num_splits is None
+             and (split_policy == "cost_model" or (split_policy == "auto" and not is_causal)))
+    return tuple(lengths) if wants else None

@@ -164,16 +164,43 @@ class GatherAttention:
         return self.attention(q, dense_k, dense_v, self._plan.table, device_lengths)
 
 
-def build_gather_attention(case, dtype_name, inputs, cube, splits, device_index):
+def check_packed_rows(k_cache, v_cache, block_table, plan: _PackPlan, page_size, dense_k,
+                      dense_v) -> None:
+    """Row-exact check of one packing (external_cache_gather.py:55-64): the
+    packed rows of request i are the pool pages table[i, :ceil(len_i / page)]
+    in order, bit for bit (NaN payloads included); a page id outside the pool
+    packs as a zero page. Raises AssertionError naming the first request and
+    tensor that differ. Runs on the device, outside any timed call."""
+    pool_pages = k_cache.shape[0] // page_size
+    h, d = k_cache.shape[1:]
+    bits = torch.int16  # fp16 / bf16 compared as raw 16-bit patterns
+    for name, original, packed in (("K", k_cache, dense_k), ("V", v_cache, dense_v)):
+        pages = original.view(pool_pages, page_size, h, d)
+        for i in range(len(plan.offsets) - 1):
+            count = (plan.offsets[i + 1] - plan.offsets[i]) // page_size
+            if not count:
+                continue
+            ids = block_table[i, :count].long()
+            inside = (ids >= 0) & (ids < pool_pages)
+            expected = pages[ids.clamp(0, pool_pages - 1)]
+            expected = torch.where(inside.view(-1, 1, 1, 1), expected, torch.zeros_like(expected))
+            got = packed[plan.offsets[i]:plan.offsets[i + 1]].view(count, page_size, h, d)
+            if not torch.equal(got.view(bits), expected.view(bits)):
+                raise AssertionError(f"packed {name} rows of request {i} differ from its pool pages")
+
+
+def build_gather_attention(case, dtype_name, inputs, cube, splits, device_index, *, check=True):
     """Plan the packing and the attention over the packed cache.
 
     The arguments and the (callable, info) result are those of the reference
     helper (external_cache_gather.py:14, :70-77): case = (name, B, Sq, H, D,
     page, width, lengths, causal) with host lengths, inputs = (q, k, v, table,
     device lengths), cube = a module with build_kernel (for example
-    fgw_amd.operators.mha.current). The callable is a GatherAttention. The
-    packed rows are not read back here: a caller that wants them checked
-    compares GatherAttention.pack() with the pool pages itself.
+    fgw_amd.operators.mha.current). The callable is a GatherAttention. As in
+    the reference helper, one packing is made and checked row-exactly against
+    the pool pages before the callable is returned (check_packed_rows;
+    info["gather_accuracy"] = "exact_passed"); check=False skips it
+    ("unchecked").
     """
     _, b, sq, h, d, page, width, lengths, causal = case
     q, k, v, table, device_lengths = inputs
@@ -183,8 +210,12 @@ def build_gather_attention(case, dtype_name, inputs, cube, splits, device_index)
     attention = cube.build_kernel(b, sq, h, d, plan.rows, width, page, causal, dtype_name,
                                   device_index, num_splits=splits)
     runner = GatherAttention(q, k, v, table, device_lengths, plan, page, attention)
+    if check:
+        dense_k, dense_v = runner.pack()
+        check_packed_rows(k, v, table, plan, page, dense_k, dense_v)
     return runner, {
-        "factory": "fgw_mha_pack_pages", "gather_accuracy": "unchecked",
+        "factory": "fgw_mha_pack_pages",
+        "gather_accuracy": "exact_passed" if check else "unchecked",
         "gather_calls_per_attention": 1 if plan.total_pages else 0,
         "packed_rows": plan.offsets[-1], "live_rows": sum(lengths),
         "num_splits": attention.num_splits,

@@ -349,3 +349,38 @@ def test_plan_automatic_tile_balanced_causal_splits(lib):
     # An explicit split count keeps even splits.
     assert _lib.plan(shape(b=1, h=8, sq=4096, kv=4096, causal=1), _lib.Request(2, -1, -1),
                      DEVICE).split_keys == 0
+
+
+def test_cost_model_plans_receive_host_lengths_causal_or_not():
+    """An explicit cost_model call plans with the host lengths whether or not
+    it is causal (v7_experimental.py:885-886); 'auto' forwards them only for
+    non-causal calls; full caches and explicit split counts never."""
+    from fgw_amd.operators.mha.kernels.mha_paged_decode_hip import planning_lengths
+    ragged = [100, 3000]
+    assert planning_lengths(ragged, False, None, "cost_model", True) == (100, 3000)
+    assert planning_lengths(ragged, False, None, "cost_model", False) == (100, 3000)
+    assert planning_lengths(ragged, False, None, "auto", False) == (100, 3000)
+    assert planning_lengths(ragged, False, None, "auto", True) is None
+    assert planning_lengths(ragged, False, None, "legacy", False) is None
+    assert planning_lengths(ragged, False, 4, "cost_model", True) is None
+    assert planning_lengths([4096, 4096], True, None, "cost_model", False) is None
+
+
+def test_cost_model_with_an_explicit_layout_keeps_that_layout(lib, monkeypatch):
+    """The cost model's move to the single-stage kernel applies to the key
+    layout only: with layout='query' or 'prefill' the plan keeps the layout's
+    own kernel instead of requesting a stage count the planner refuses."""
+    from fgw_amd.operators.mha.kernels import mha_paged_decode_hip as K
+    monkeypatch.setattr(K, "_device_info", lambda index: DEVICE)
+    kv = 32768
+    args = (2, 1, 8, 128, 2 * kv, kv // 128, 128, False, "bfloat16", 0)
+    auto = K.build_kernel(*args, split_policy="cost_model", full_kv_cache=True)
+    assert auto.layout == "key" and auto.stages == 1
+    for layout in ("query", "key"):
+        kern = K.build_kernel(*args, split_policy="cost_model", full_kv_cache=True, layout=layout)
+        assert kern.layout == layout
+        assert kern.stages == (1 if layout == "key" else 2)
+    sq = 512  # the prefill layout needs Sq > 128 to be worth asking for; any Sq plans
+    pre = K.build_kernel(2, sq, 8, 128, 2 * kv, kv // 128, 128, False, "bfloat16", 0,
+                         split_policy="cost_model", full_kv_cache=True, layout="prefill")
+    assert pre.layout == "prefill"

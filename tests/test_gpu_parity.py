@@ -97,6 +97,16 @@ def test_forced_splits(splits):
                 run_case(case, 7, dtype, causal, "full", num_splits=splits)
 
 
+def test_cost_model_policy_on_causal_ragged_calls():
+    """split_policy='cost_model' with causal, ragged lengths plans with the
+    host lengths (v7_experimental.py:885-886) and matches the oracle."""
+    for name in ("split_d16_q1", "split_d128_q33", "split_d48_q17", "cube_decode2048"):
+        case = C.ALL_CASES[name]
+        for dtype in DTYPES:
+            run_case(case, 7, dtype, True, "mixed", split_policy="cost_model")
+            run_case(case, 11, dtype, False, "mixed", split_policy="cost_model")
+
+
 def test_gather_bit_exact():
     from fgw_amd import _lib
     lib = _lib.load()

@@ -103,6 +103,7 @@ def test_gather_attention_matches_paged_attention(name, causal, splits):
     combined, info = P.build_gather_attention(
         (name, b, sq, h, d, p, w, lengths, causal), "bfloat16", inputs, current, splits, 0)
     assert info["live_rows"] == sum(lengths) and info["packed_rows"] == combined.packed_rows
+    assert info["gather_accuracy"] == "exact_passed"
     # The packed rows, row-exact against the pool pages (external_cache_gather.py:55-64).
     dense_k, dense_v = combined.pack()
     ek, ev, offsets = O.pack_pages(k, v, table, lengths, p)
@@ -114,3 +115,32 @@ def test_gather_attention_matches_paged_attention(name, causal, splits):
     expected = O.reference(q, k, v, table, lt, p, causal)
     rtol, atol = O.TOLERANCES[dtype]
     torch.testing.assert_close(got.cpu(), expected, rtol=rtol, atol=atol)
+
+
+def test_packed_row_check_on_host_tensors():
+    """check_packed_rows (the reference helper's row-exact check,
+    external_cache_gather.py:55-64) accepts the oracle's packing, NaN rows and
+    zero pages for ids outside the pool included, and names the request of a
+    single flipped bit."""
+    g = torch.Generator().manual_seed(9)
+    page, h, d = 16, 2, 32
+    k = torch.randn(5 * page, h, d, generator=g).bfloat16()
+    v = torch.randn(5 * page, h, d, generator=g).bfloat16()
+    k[3 * page + 2, 1, 5] = float("nan")
+    table = torch.tensor([[3, 2, 0], [1, 0, 4]], dtype=torch.int32)
+    lengths = [40, 20]
+    ek, ev, offsets = O.pack_pages(k, v, table, lengths, page)
+    plan = P._PackPlan(offsets, ek.shape[0], None, None, offsets[-1] // page)
+    P.check_packed_rows(k, v, table, plan, page, ek, ev)
+    # Page ids -1 and 9 lie outside the 5-page pool: their packed pages are zero.
+    outside = torch.tensor([[3, -1, 9], [1, 0, 4]], dtype=torch.int32)
+    zk, zv = ek.clone(), ev.clone()
+    zk[page:3 * page] = 0
+    zv[page:3 * page] = 0
+    P.check_packed_rows(k, v, outside, plan, page, zk, zv)
+    with pytest.raises(AssertionError, match="K rows of request 0"):
+        P.check_packed_rows(k, v, outside, plan, page, ek, ev)
+    bad = ev.clone()
+    bad.view(torch.int16)[offsets[1] + 3, 0, 7] ^= 1
+    with pytest.raises(AssertionError, match="V rows of request 1"):
+        P.check_packed_rows(k, v, table, plan, page, ek, bad)
