@@ -10,10 +10,11 @@ import pathlib
 import threading
 
 LIBRARY = pathlib.Path(__file__).resolve().with_name("libfgw_mha.so")
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 FGW_MHA_OK, FGW_MHA_EINVAL, FGW_MHA_EUNSUPPORTED, FGW_MHA_EHIP = 0, -1, -2, -3
 NOALLOC_SCRATCH_BYTES = 32 << 20  # FGW_MHA_NOALLOC_SCRATCH_BYTES
+NOALLOC_ARRIVALS = 65536  # FGW_MHA_NOALLOC_ARRIVALS
 DTYPE_FLOAT16, DTYPE_BFLOAT16 = 0, 1
 LAYOUT_AUTO, LAYOUT_QUERY, LAYOUT_KEY, LAYOUT_PREFILL = -1, 0, 1, 2
 NUM_LAYOUTS = 3
@@ -43,13 +44,13 @@ class Plan(ctypes.Structure):
                 ("work_items", c_int32), ("grid", c_int32), ("threads", c_int32),
                 ("execution_mode", c_int32), ("dim_padded", c_int32),
                 ("parts_floats", c_int64), ("lse_floats", c_int64), ("split_keys", c_int32),
-                ("stages", c_int32)]
+                ("stages", c_int32), ("arrival_counters", c_int32)]
 
 
 class Tensors(ctypes.Structure):
     _fields_ = [("q", c_void_p), ("k_cache", c_void_p), ("v_cache", c_void_p),
                 ("block_table", c_void_p), ("cache_seqlens", c_void_p), ("out", c_void_p),
-                ("parts", c_void_p), ("lse", c_void_p)]
+                ("parts", c_void_p), ("lse", c_void_p), ("arrivals", c_void_p)]
 
 
 class Schedule(ctypes.Structure):

@@ -73,7 +73,8 @@ def _build_shim() -> pathlib.Path:
            f"-I{tdir / 'include'}", f"-I{tdir / 'include' / 'torch' / 'csrc' / 'api' / 'include'}",
            "-I/opt/rocm/include", f"-I{sysconfig.get_paths()['include']}",
            str(SHIM_SOURCE), "-o", str(tmp), f"-L{tdir / 'lib'}", f"-Wl,-rpath,{tdir / 'lib'}",
-           "-lc10", "-lc10_hip", "-ltorch_cpu", "-ltorch_python"]
+           "-lc10", "-lc10_hip", "-ltorch_cpu", "-ltorch_python",
+           "-L/opt/rocm/lib", "-Wl,-rpath,/opt/rocm/lib", "-lamdhip64"]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"launch shim build failed:\n{proc.stdout}{proc.stderr}")

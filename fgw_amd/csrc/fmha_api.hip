@@ -134,14 +134,20 @@ constexpr int kMinRoundsPerSplitPrefill = 4;
 // address. It uses the address hipGetSymbolAddress returns on each device.
 constexpr int64_t kScratchFloats = FGW_MHA_NOALLOC_SCRATCH_BYTES / 4;
 static __device__ __align__(256) float scratch[kScratchFloats];
+// Its fused-merge arrival counters (one per task): zero when the code object
+// is loaded, and every call returns the counters it used to zero.
+constexpr int kScratchArrivals = FGW_MHA_NOALLOC_ARRIVALS;
+static __device__ __align__(256) int32_t arrival_scratch[kScratchArrivals] = {};
 
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mutex;
 float* g_scratch_ptr[kMaxDevices] = {};
+int32_t* g_arrival_ptr[kMaxDevices] = {};
 
-// This device's address of `scratch`, looked up once per device with that
-// device current (the caller's current device is restored).
-int scratch_address(int device, float** out) {
+// This device's addresses of `scratch` and `arrival_scratch`, looked up once
+// per device with that device current (the caller's current device is
+// restored).
+int scratch_address(int device, float** out, int32_t** arrivals) {
   if (device < 0 || device >= kMaxDevices)
     return fail(FGW_MHA_EUNSUPPORTED, "device %d is outside the scratch table", device);
   std::lock_guard<std::mutex> lock(g_scratch_mutex);
@@ -152,13 +158,17 @@ int scratch_address(int device, float** out) {
     if (current != device && (err = hipSetDevice(device)) != hipSuccess)
       return hip_fail(err, "hipSetDevice");
     void* ptr = nullptr;
+    void* aptr = nullptr;
     err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err == hipSuccess) err = hipGetSymbolAddress(&aptr, HIP_SYMBOL(arrival_scratch));
     if (current != device) (void)hipSetDevice(current);
     if (err != hipSuccess) return hip_fail(err, "hipGetSymbolAddress(scratch)");
-    if (!ptr) return fail(FGW_MHA_EHIP, "hipGetSymbolAddress(scratch) returned NULL");
+    if (!ptr || !aptr) return fail(FGW_MHA_EHIP, "hipGetSymbolAddress(scratch) returned NULL");
+    g_arrival_ptr[device] = static_cast<int32_t*>(aptr);
     g_scratch_ptr[device] = static_cast<float*>(ptr);
   }
   *out = g_scratch_ptr[device];
+  *arrivals = g_arrival_ptr[device];
   return FGW_MHA_OK;
 }
 
@@ -180,22 +190,25 @@ int default_stages(int layout, int dpad) {
 // The key layout's single-stage variant exists for head-dim tile 128.
 bool has_key_single(int layout, int dpad) { return layout == kLayoutKey && dpad == 128; }
 
-// Automatic plans of short decode (Sq <= 4) on the key layout at head-dim
+// Automatic plans of short decode (Sq <= 16) on the key layout at head-dim
 // tile 128 whose even splits number 16 or more and give each CU at most one
-// work item move to the single-stage kernel with 4x the splits (each keeping
-// >= 512 keys), else 2x (>= 256 keys); returns that split count, or 0 to keep
+// work item move to the single-stage kernel with more splits: for Sq <= 4,
+// 4x the splits (each keeping >= 512 keys), else 2x (>= 256 keys); for
+// 4 < Sq <= 16, 2x (>= 256 keys). Returns that split count, or 0 to keep
 // the plan. Two workgroups per CU then overlap one's prologue and epilogue
 // with the other's stream. Measured (single-call median, same box, A/B):
 // B2 H8 KV 32768 0.962-0.965x (BF16 and FP16), KV 65536 0.975x, KV 16384
 // 0.981x, KV 8192 0.972x, B1 H8 / B2 H4 KV 32768 0.993x, B1 H16 Q4 0.987x;
-// below 16 splits (B2 H16 or B8 H8, 4-8 splits) and at Sq 16 it measured
-// 1.00-1.05x, so those plans stay.
+// B2 H8 Q8 / Q16 at 2x (32 splits): KV 32768 0.976x / 0.975x, KV 8192
+// 0.969x / 0.966x, where 4x (64 splits) lost at Q16 (1.03x); below 16
+// splits (B2 H16 or B8 H8, 4-8 splits) it measured 1.00-1.05x, so those
+// plans stay.
 int single_stage_splits(const fgw_mha_shape* s, const fgw_mha_device_info* dev, int layout,
                         int dpad, int64_t tasks, int splits, int64_t capacity) {
-  if (!has_key_single(layout, dpad) || s->sq > 4 || splits < 16 ||
+  if (!has_key_single(layout, dpad) || s->sq > 16 || splits < 16 ||
       dev->wg_per_cu_key_single < 2 || tasks * splits > dev->num_cus)
     return 0;
-  if (4 * splits <= kMaxSplits && capacity / (4 * splits) >= 512) return 4 * splits;
+  if (s->sq <= 4 && 4 * splits <= kMaxSplits && capacity / (4 * splits) >= 512) return 4 * splits;
   if (2 * splits <= kMaxSplits && capacity / (2 * splits) >= 256) return 2 * splits;
   return 0;
 }
@@ -212,6 +225,38 @@ int rows_per_tile(int layout) {
 }
 // Head-dim tiles with a prefill-layout kernel.
 bool has_prefill(int dpad) { return dpad == 64 || dpad == 128; }
+
+// Largest split chunk of the fused merge in the kernels of a head-dim tile.
+int fused_max_chunk(int dpad) {
+  switch (dpad) {
+    case 32: return kFusedMergeMaxChunk<32>;
+    case 64: return kFusedMergeMaxChunk<64>;
+    case 128: return kFusedMergeMaxChunk<128>;
+    default: return kFusedMergeMaxChunk<256>;
+  }
+}
+
+// Arrival counter buffer (int32 elements: kArrivalStride per task) of a split
+// plan whose merge fgw_mha_fwd fuses into the partial kernel (the last work
+// item of each task merges the task's rows, arrive_and_merge in
+// fmha_kernel.h), or 0 to merge in a second launch. Fused for key-layout
+// plans of Sq <= 2 with at most kMergeChunk splits (one round of the
+// per-thread merge), where it measured level with or faster than the second
+// launch (B2 H8 D128 BF16, KV 2048-32768, 4-16 splits of either key kernel,
+// 36 plans: single-call median 0.990x on geometric mean, 0.963-1.071x;
+// back to back 0.970x). Elsewhere it lost: every work item waits for its
+// partial stores to complete and for the count before its workgroup ends,
+// and the last one merges alone; with more splits per task (32-128 splits:
+// 1.158x, 1.01-1.51x) or more rows to merge (Sq 4-16: 1.074x, 0.97-1.47x)
+// that tail exceeds the second launch. Kernels whose fused merge leaves out
+// the 16-split chunk (kFusedMergeMaxChunk) fuse at most 8 splits.
+int64_t fused_merge_counters(const fgw_mha_shape* s, int layout, int splits, int rows,
+                             int64_t tasks) {
+  (void)rows;
+  if (splits < 2 || layout != kLayoutKey || s->sq > 2 || splits > kMergeChunk) return 0;
+  if (splits > fused_max_chunk(dim_tile(s->dim))) return 0;
+  return tasks * kArrivalStride;
+}
 
 // split_keys > 0 means length-balanced splits in the key layout and
 // tile-balanced causal splits in the prefill layout.
@@ -343,7 +388,9 @@ int check_plan(const fgw_mha_shape* s, const fgw_mha_plan_t* p) {
       p->grid < 1 || p->grid > p->work_items ||
       p->dim_padded != dim_tile(s->dim) || p->execution_mode != (p->num_splits > 1 ? 1 : 0) ||
       !split_keys_valid(s, p->layout, p->num_splits, p->split_keys) ||
-      !stages_valid(p->layout, p->dim_padded, p->stages))
+      !stages_valid(p->layout, p->dim_padded, p->stages) ||
+      (p->arrival_counters != 0 &&
+       p->arrival_counters != fused_merge_counters(s, p->layout, p->num_splits, rows, tasks)))
     return fail(FGW_MHA_EINVAL, "plan does not match the shape; call fgw_mha_plan");
   return FGW_MHA_OK;
 }
@@ -394,6 +441,7 @@ FwdParams make_params(const fgw_mha_shape* s, const fgw_mha_plan_t* p, const fgw
   f.seg_offsets = nullptr;
   f.slots = 0;
   f.seg_scale = 1;
+  f.arrivals = nullptr;
   return f;
 }
 
@@ -420,12 +468,13 @@ int check_schedule(const fgw_mha_shape* s, const fgw_mha_schedule* sc) {
 // tile-balanced plan's one-split tiles then write their output directly).
 int launch_partial_kernel(const fgw_mha_shape* s, const fgw_mha_plan_t* p,
                           const fgw_mha_tensors* t, int mode, hipStream_t stream,
-                          bool whole = false) {
+                          bool whole = false, int32_t* arrivals = nullptr) {
   const int stages = p->stages == default_stages(p->layout, p->dim_padded) ? 0 : p->stages;
   const FwdEntry e = fwd_entry(s->dtype == FGW_MHA_BFLOAT16, p->dim_padded, p->layout, stages);
   if (!e.launch) return fail(FGW_MHA_EUNSUPPORTED, "no kernel for dim tile %d", p->dim_padded);
   FwdParams f = make_params(s, p, t, mode);
   f.split_direct = whole && mode == 1 && tile_balanced(p->layout, s->causal, p->split_keys);
+  f.arrivals = mode == 1 ? arrivals : nullptr;
   const hipError_t err = e.launch(f, p->grid, stream);
   return err == hipSuccess ? FGW_MHA_OK : hip_fail(err, "forward kernel launch");
 }
@@ -616,6 +665,7 @@ int fgw_mha_plan(const fgw_mha_shape* s, const fgw_mha_request* req,
   out->lse_floats = splits > 1 ? (int64_t)s->batch * s->heads * splits * s->sq : 0;
   out->split_keys = split_keys;
   out->stages = stages;
+  out->arrival_counters = (int32_t)fused_merge_counters(s, layout, splits, rows, tasks);
   return FGW_MHA_OK;
 }
 
@@ -626,6 +676,8 @@ int fgw_mha_fwd(const fgw_mha_shape* s, const fgw_mha_plan_t* p, const fgw_mha_t
   if (!rc) rc = check_tensors(t, true, true, p->num_splits > 1);
   if (rc) return rc;
   if (p->num_splits == 1) return launch_partial_kernel(s, p, t, 0, stream);
+  if (t->arrivals && p->arrival_counters > 0)  // one launch: the last work item merges
+    return launch_partial_kernel(s, p, t, 1, stream, true, t->arrivals);
   rc = launch_partial_kernel(s, p, t, 1, stream, true);
   if (rc) return rc;
   return launch_merge_kernel(s, p, t, stream, true);
@@ -648,11 +700,14 @@ int fgw_mha_fwd_noalloc(const fgw_mha_shape* s, const fgw_mha_plan_t* p,
   hipError_t err = stream ? hipStreamGetDevice(stream, &device) : hipGetDevice(&device);
   if (err != hipSuccess) return hip_fail(err, "stream device");
   float* base = nullptr;
-  rc = scratch_address(device, &base);
+  int32_t* arrivals = nullptr;
+  rc = scratch_address(device, &base, &arrivals);
   if (rc) return rc;
   fgw_mha_tensors w = *t;
   w.parts = base;  // 256-byte aligned
   w.lse = base + p->parts_floats;
+  if (p->arrival_counters > 0 && p->arrival_counters <= kScratchArrivals)
+    return launch_partial_kernel(s, p, &w, 1, stream, true, arrivals);
   rc = launch_partial_kernel(s, p, &w, 1, stream, true);
   if (rc) return rc;
   return launch_merge_kernel(s, p, &w, stream, true);

@@ -4,110 +4,7 @@
 
 namespace fgw_mha {
 
-// LSE merge of the split partials of output rows [q0, q0 + rows) of (b, h),
-// one (row, 4 dims) pair per thread:
-//   peak = max over splits with LSE > -1e29,
-//   w_s  = LSE_s > -1e29 ? exp(LSE_s - peak) : 0,
-//   O    = sum_s w_s * Part_s / max(sum_s w_s, 1e-30), cast to the input dtype.
-// This is the reference merge (v7.py:352-370, cube_general.py:259-278):
-// splits are taken in chunks of kMergeChunk whose loads are all issued before
-// any is used (one memory round trip per chunk), and the running peak moves
-// once per chunk. Empty splits (LSE -1e30) carry zero weight and an
-// all-empty row is exactly zero.
-constexpr int kMergeChunk = 16;
-// One (row, 4 dims): split s's LSE at ls[s * lse_stride], its part at
-// ps[s * part_stride]; the result goes to dst in the input dtype. Chunks of
-// CH splits; the loads of a chunk's missing splits past `splits` are
-// clamped to the last split and carry weight 0.
-template <bool BF16, int CH>
-__device__ __forceinline__ void merge_one_chunked(const float* ls, int64_t lse_stride,
-                                                  const float* ps, int64_t part_stride,
-                                                  int splits, u16* dst) {
-  using E = Elem<BF16>;
-  float peak = kNegBig, tot = 0.0f;
-  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int s0 = 0; s0 < splits; s0 += CH) {
-    float x[CH];
-    f32x4 v[CH];
-#pragma unroll
-    for (int i = 0; i < CH; ++i) {
-      const int s = s0 + i < splits ? s0 + i : splits - 1;  // clamped; weight 0 below
-      x[i] = ls[(int64_t)s * lse_stride];
-      v[i] = *reinterpret_cast<const f32x4*>(ps + (int64_t)s * part_stride);
-    }
-    float cpeak = peak;
-#pragma unroll
-    for (int i = 0; i < CH; ++i) {
-      const bool live = s0 + i < splits && x[i] > -1.0e29f;
-      cpeak = live ? fmaxf(cpeak, x[i]) : cpeak;
-    }
-    const float keep = expf(peak - cpeak);  // 0 while nothing was live, 1 if unchanged
-    tot *= keep;
-    acc *= keep;
-#pragma unroll
-    for (int i = 0; i < CH; ++i) {
-      const bool live = s0 + i < splits && x[i] > -1.0e29f;
-      const float wgt = live ? expf(x[i] - cpeak) : 0.0f;
-      tot += wgt;
-      acc += live ? v[i] * wgt : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    }
-    peak = cpeak;
-  }
-  const float inv = 1.0f / fmaxf(tot, 1.0e-30f);
-  u32x2 w;
-  w.x = E::pack2(acc[0] * inv, acc[1] * inv);
-  w.y = E::pack2(acc[2] * inv, acc[3] * inv);
-  *reinterpret_cast<u32x2*>(dst) = w;
-}
-
-// merge_one_chunked with the smallest chunk of 2, 4, 8 or 16 that holds all
-// `splits` (one chunk up to 16): a chunk of 16 for 2 splits would issue
-// eight times the loads (the clamped ones), which the prefill-length merges
-// of few splits feel. The live splits are summed in the same order whatever
-// the chunk (a larger chunk only adds zeros for its dead splits).
-template <bool BF16>
-__device__ __forceinline__ void merge_one(const float* ls, int64_t lse_stride, const float* ps,
-                                          int64_t part_stride, int splits, u16* dst) {
-  if (splits <= 2)
-    merge_one_chunked<BF16, 2>(ls, lse_stride, ps, part_stride, splits, dst);
-  else if (splits <= 4)
-    merge_one_chunked<BF16, 4>(ls, lse_stride, ps, part_stride, splits, dst);
-  else if (splits <= 8)
-    merge_one_chunked<BF16, 8>(ls, lse_stride, ps, part_stride, splits, dst);
-  else
-    merge_one_chunked<BF16, kMergeChunk>(ls, lse_stride, ps, part_stride, splits, dst);
-}
-
-// Splits row (b, ., q) of a merge reads: all slots, the balanced count of
-// request b (balanced_splits over its clamped length), or the slots of q's
-// query tile in a tile-balanced causal plan.
-__device__ __forceinline__ int merge_splits(const MergeParams& p, int b, int q) {
-  if (p.split_keys <= 0) return p.splits;
-  if (p.rows_tile > 0)
-    return tile_slots(q / p.rows_tile, p.sq, p.capacity, p.rows_tile, p.split_keys, p.splits);
-  int len = p.lengths[b];
-  len = len < 0 ? 0 : (len > p.capacity ? p.capacity : len);
-  return balanced_splits(len, p.split_keys, p.splits);
-}
-
-// Rows [q0, q0 + rows) of (b, h): `slots` is the workspace's split dimension,
-// the first `used` slots are merged.
-template <bool BF16>
-__device__ __forceinline__ void merge_rows(const float* parts, const float* lse, void* out, int sq,
-                                           int heads, int dim, int slots, int used, int b, int h,
-                                           int q0, int rows, int tid, int nthreads) {
-  const int d4n = dim / 4;
-  const int64_t bhs = ((int64_t)b * heads + h) * slots;
-  for (int idx = tid; idx < rows * d4n; idx += nthreads) {
-    const int q = q0 + idx / d4n, d0 = 4 * (idx % d4n);
-    u16* dst = static_cast<u16*>(out) + (((int64_t)b * sq + q) * heads + h) * dim + d0;
-    merge_one<BF16>(lse + bhs * sq + q, sq, parts + (bhs * sq + q) * dim + d0,
-                    (int64_t)sq * dim, used, dst);
-  }
-}
-
 // Stand-alone LSE merge: one workgroup per (b, h, group of rows_per_wg rows).
-constexpr int kMergeThreads = 256;
 template <bool BF16>
 __global__ __launch_bounds__(kMergeThreads) void merge_kernel(MergeParams p, int rows_per_wg) {
   const int groups = (p.sq + rows_per_wg - 1) / rows_per_wg;
@@ -122,109 +19,18 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(MergeParams p, int
                    bh % p.heads, q0, rows, threadIdx.x, kMergeThreads);
 }
 
-// LSE merge of one output row (b, h, q) per workgroup with the splits spread
-// over the threads, for split counts above kMergeChunk (where merge_one
-// would take one memory round trip per chunk). Thread (g, c), g < G =
-// kMergeThreads / (D / 4), takes dims 4c .. 4c + 3 of splits g, g + G, ...
-// and folds them as merge_one does (running peak per chunk of kMergeChunk,
-// weights exp(LSE - peak), empty splits weight 0) without normalising; the
-// G group states are then rescaled to the common peak and summed in group
-// order through LDS, and O = acc / max(tot, 1e-30) is cast to the input
-// dtype. An all-empty row is exactly zero.
-// Group g's splits g, g + G, ... of a wide merge row (see merge_wide_kernel)
-// in chunks of CH whose loads are all issued before any is used; the running
-// peak moves once per chunk. Missing splits past `used` load split g again
-// and carry weight 0.
-template <int CH>
-__device__ __forceinline__ void wide_group(const float* ls, const float* ps, int64_t lse_stride,
-                                           int64_t part_stride, int g, int G, int used,
-                                           float& peak, float& tot, f32x4& acc) {
-  for (int s0 = g; s0 < used; s0 += CH * G) {
-    float x[CH];
-    f32x4 v[CH];
-#pragma unroll
-    for (int i = 0; i < CH; ++i) {
-      const int s = s0 + i * G < used ? s0 + i * G : g;  // clamped; weight 0 below
-      x[i] = ls[(int64_t)s * lse_stride];
-      v[i] = *reinterpret_cast<const f32x4*>(ps + (int64_t)s * part_stride);
-    }
-    float cpeak = peak;
-#pragma unroll
-    for (int i = 0; i < CH; ++i) {
-      const bool live = s0 + i * G < used && x[i] > -1.0e29f;
-      cpeak = live ? fmaxf(cpeak, x[i]) : cpeak;
-    }
-    const float keep = expf(peak - cpeak);
-    tot *= keep;
-    acc *= keep;
-#pragma unroll
-    for (int i = 0; i < CH; ++i) {
-      const bool live = s0 + i * G < used && x[i] > -1.0e29f;
-      const float wgt = live ? expf(x[i] - cpeak) : 0.0f;
-      tot += wgt;
-      acc += live ? v[i] * wgt : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    }
-    peak = cpeak;
-  }
-}
-
 template <bool BF16>
 __global__ __launch_bounds__(kMergeThreads) void merge_wide_kernel(MergeParams p) {
-  using E = Elem<BF16>;
   __shared__ float speak[kMergeThreads];
   __shared__ float stot[kMergeThreads];
   __shared__ f32x4 sacc[kMergeThreads];
-  const int d4n = p.dim / 4;
-  const int G = kMergeThreads / d4n;
-  const int t = threadIdx.x, c = t % d4n, g = t / d4n;
-  const bool act = g < G;
   const int q = (int)(blockIdx.x % (unsigned)p.sq);
   const int bh = (int)(blockIdx.x / (unsigned)p.sq);
   const int b = bh / p.heads, h = bh % p.heads;
-  const int64_t base = (int64_t)bh * p.splits * p.sq + q;  // (b, h, split 0, q)
-  const float* ls = p.lse + base;
-  const float* ps = p.parts + base * p.dim + 4 * c;
-  const int64_t part_stride = (int64_t)p.sq * p.dim;
   const int used = merge_splits(p, b, q);
   if (p.skip_single && used == 1) return;  // written by the forward kernel (whole workgroup)
-  float peak = kNegBig, tot = 0.0f;
-  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-  if (act) {
-    // The smallest chunk of 4, 8 or 16 that holds a group's splits (16
-    // beyond): 64 splits over 8 groups are one chunk of 8, not 16 with half
-    // of the loads clamped. The live splits are summed in the same order.
-    const int per = (used + G - 1) / G;
-    if (per <= 4)
-      wide_group<4>(ls, ps, p.sq, part_stride, g, G, used, peak, tot, acc);
-    else if (per <= 8)
-      wide_group<8>(ls, ps, p.sq, part_stride, g, G, used, peak, tot, acc);
-    else
-      wide_group<kMergeChunk>(ls, ps, p.sq, part_stride, g, G, used, peak, tot, acc);
-    if (c == 0) speak[g] = peak;  // the same in every thread of the group
-  }
-  __syncthreads();
-  float top = kNegBig;
-  for (int k = 0; k < G; ++k) top = fmaxf(top, speak[k]);
-  if (act) {
-    const float scale = expf(peak - top);  // 0 for an empty group below a live peak
-    sacc[t] = acc * scale;
-    if (c == 0) stot[g] = tot * scale;
-  }
-  __syncthreads();
-  if (g == 0) {
-    f32x4 a = {0.0f, 0.0f, 0.0f, 0.0f};
-    float total = 0.0f;
-    for (int k = 0; k < G; ++k) {
-      a += sacc[k * d4n + c];
-      total += stot[k];
-    }
-    const float inv = 1.0f / fmaxf(total, 1.0e-30f);
-    u32x2 w;
-    w.x = E::pack2(a[0] * inv, a[1] * inv);
-    w.y = E::pack2(a[2] * inv, a[3] * inv);
-    u16* dst = static_cast<u16*>(p.out) + (((int64_t)b * p.sq + q) * p.heads + h) * p.dim + 4 * c;
-    *reinterpret_cast<u32x2*>(dst) = w;
-  }
+  merge_wide_row<BF16>(p.parts, p.lse, p.out, p.sq, p.heads, p.dim, p.splits, used, b, h, q,
+                       threadIdx.x, speak, stot, sacc);
 }
 
 // Merge of the static schedule's split tiles: group g (task, first slot,

@@ -564,7 +564,14 @@ __device__ __forceinline__ void store_row(const FwdParams& p, int b, int h, int 
   } else {
     float* dst = p.parts +
                  ((((int64_t)b * p.heads + h) * p.splits + split) * p.sq + qrow) * p.dim + d0;
-    *reinterpret_cast<f32x4*>(dst) = val * inv;
+    const f32x4 x = val * inv;
+    if (p.arrivals != nullptr) {  // fused merge: coherent at the device (arrive_and_merge)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        __hip_atomic_store(dst + i, x[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+      *reinterpret_cast<f32x4*>(dst) = x;
+    }
   }
 }
 
@@ -713,6 +720,287 @@ __device__ void balanced_prefix(const FwdParams& p, const int32_t* lengths, int 
     if (lane == 63) pre[p.batch] = incl;
   }
   __syncthreads();
+}
+
+// LSE merge of the split partials of output rows [q0, q0 + rows) of (b, h),
+// one (row, 4 dims) pair per thread:
+//   peak = max over splits with LSE > -1e29,
+//   w_s  = LSE_s > -1e29 ? exp(LSE_s - peak) : 0,
+//   O    = sum_s w_s * Part_s / max(sum_s w_s, 1e-30), cast to the input dtype.
+// This is the reference merge (v7.py:352-370, cube_general.py:259-278):
+// splits are taken in chunks of kMergeChunk whose loads are all issued before
+// any is used (one memory round trip per chunk), and the running peak moves
+// once per chunk. Empty splits (LSE -1e30) carry zero weight and an
+// all-empty row is exactly zero.
+constexpr int kMergeChunk = 16;
+// One (row, 4 dims): split s's LSE at ls[s * lse_stride], its part at
+// ps[s * part_stride]; the result goes to dst in the input dtype. Chunks of
+// CH splits; the loads of a chunk's missing splits past `splits` are
+// clamped to the last split and carry weight 0.
+// Split state loads of a merge. COH (the fused merge): agent-scope relaxed
+// atomic loads, which read the partials other XCDs' workgroups wrote with
+// agent-scope stores without any cache write-back or invalidation; else
+// plain loads (a separate launch sees everything the forward kernel wrote).
+template <bool COH>
+__device__ __forceinline__ float merge_ld1(const float* p) {
+  if constexpr (COH) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return *p;
+}
+template <bool COH>
+__device__ __forceinline__ f32x4 merge_ld4(const float* p) {
+  if constexpr (COH)
+    return f32x4{merge_ld1<true>(p), merge_ld1<true>(p + 1), merge_ld1<true>(p + 2),
+                 merge_ld1<true>(p + 3)};
+  return *reinterpret_cast<const f32x4*>(p);
+}
+
+template <bool BF16, int CH, bool COH = false>
+__device__ __forceinline__ void merge_one_chunked(const float* ls, int64_t lse_stride,
+                                                  const float* ps, int64_t part_stride,
+                                                  int splits, u16* dst) {
+  using E = Elem<BF16>;
+  float peak = kNegBig, tot = 0.0f;
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int s0 = 0; s0 < splits; s0 += CH) {
+    float x[CH];
+    f32x4 v[CH];
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int s = s0 + i < splits ? s0 + i : splits - 1;  // clamped; weight 0 below
+      x[i] = merge_ld1<COH>(ls + (int64_t)s * lse_stride);
+      v[i] = merge_ld4<COH>(ps + (int64_t)s * part_stride);
+    }
+    float cpeak = peak;
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const bool live = s0 + i < splits && x[i] > -1.0e29f;
+      cpeak = live ? fmaxf(cpeak, x[i]) : cpeak;
+    }
+    const float keep = expf(peak - cpeak);  // 0 while nothing was live, 1 if unchanged
+    tot *= keep;
+    acc *= keep;
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const bool live = s0 + i < splits && x[i] > -1.0e29f;
+      const float wgt = live ? expf(x[i] - cpeak) : 0.0f;
+      tot += wgt;
+      acc += live ? v[i] * wgt : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    peak = cpeak;
+  }
+  const float inv = 1.0f / fmaxf(tot, 1.0e-30f);
+  u32x2 w;
+  w.x = E::pack2(acc[0] * inv, acc[1] * inv);
+  w.y = E::pack2(acc[2] * inv, acc[3] * inv);
+  *reinterpret_cast<u32x2*>(dst) = w;
+}
+
+// merge_one_chunked with the smallest chunk of 2, 4, 8 or 16 that holds all
+// `splits` (one chunk up to 16): a chunk of 16 for 2 splits would issue
+// eight times the loads (the clamped ones), which the prefill-length merges
+// of few splits feel. The live splits are summed in the same order whatever
+// the chunk (a larger chunk only adds zeros for its dead splits).
+// MAXCH < kMergeChunk leaves the 16-split chunk out (fewer registers); the
+// caller then never merges more than 8 splits this way.
+template <bool BF16, int MAXCH = kMergeChunk, bool COH = false>
+__device__ __forceinline__ void merge_one(const float* ls, int64_t lse_stride, const float* ps,
+                                          int64_t part_stride, int splits, u16* dst) {
+  if (splits <= 2)
+    merge_one_chunked<BF16, 2, COH>(ls, lse_stride, ps, part_stride, splits, dst);
+  else if (splits <= 4)
+    merge_one_chunked<BF16, 4, COH>(ls, lse_stride, ps, part_stride, splits, dst);
+  else if (MAXCH <= 8 || splits <= 8)
+    merge_one_chunked<BF16, 8, COH>(ls, lse_stride, ps, part_stride, splits, dst);
+  else
+    merge_one_chunked<BF16, kMergeChunk, COH>(ls, lse_stride, ps, part_stride, splits, dst);
+}
+
+// Splits row (b, ., q) of a merge reads: all slots, the balanced count of
+// request b (balanced_splits over its clamped length), or the slots of q's
+// query tile in a tile-balanced causal plan.
+__device__ __forceinline__ int merge_splits(const MergeParams& p, int b, int q) {
+  if (p.split_keys <= 0) return p.splits;
+  if (p.rows_tile > 0)
+    return tile_slots(q / p.rows_tile, p.sq, p.capacity, p.rows_tile, p.split_keys, p.splits);
+  int len = p.lengths[b];
+  len = len < 0 ? 0 : (len > p.capacity ? p.capacity : len);
+  return balanced_splits(len, p.split_keys, p.splits);
+}
+
+// Rows [q0, q0 + rows) of (b, h): `slots` is the workspace's split dimension,
+// the first `used` slots are merged.
+template <bool BF16, int MAXCH = kMergeChunk, bool COH = false>
+__device__ __forceinline__ void merge_rows(const float* parts, const float* lse, void* out, int sq,
+                                           int heads, int dim, int slots, int used, int b, int h,
+                                           int q0, int rows, int tid, int nthreads) {
+  const int d4n = dim / 4;
+  const int64_t bhs = ((int64_t)b * heads + h) * slots;
+  for (int idx = tid; idx < rows * d4n; idx += nthreads) {
+    const int q = q0 + idx / d4n, d0 = 4 * (idx % d4n);
+    u16* dst = static_cast<u16*>(out) + (((int64_t)b * sq + q) * heads + h) * dim + d0;
+    merge_one<BF16, MAXCH, COH>(lse + bhs * sq + q, sq, parts + (bhs * sq + q) * dim + d0,
+                    (int64_t)sq * dim, used, dst);
+  }
+}
+
+constexpr int kMergeThreads = 256;
+
+// LSE merge of one output row (b, h, q) per workgroup with the splits spread
+// over the threads, for split counts above kMergeChunk (where merge_one
+// would take one memory round trip per chunk). Thread (g, c), g < G =
+// kMergeThreads / (D / 4), takes dims 4c .. 4c + 3 of splits g, g + G, ...
+// and folds them as merge_one does (running peak per chunk of kMergeChunk,
+// weights exp(LSE - peak), empty splits weight 0) without normalising; the
+// G group states are then rescaled to the common peak and summed in group
+// order through LDS, and O = acc / max(tot, 1e-30) is cast to the input
+// dtype. An all-empty row is exactly zero.
+// Group g's splits g, g + G, ... of a wide merge row (see merge_wide_kernel)
+// in chunks of CH whose loads are all issued before any is used; the running
+// peak moves once per chunk. Missing splits past `used` load split g again
+// and carry weight 0.
+template <int CH, bool COH = false>
+__device__ __forceinline__ void wide_group(const float* ls, const float* ps, int64_t lse_stride,
+                                           int64_t part_stride, int g, int G, int used,
+                                           float& peak, float& tot, f32x4& acc) {
+  for (int s0 = g; s0 < used; s0 += CH * G) {
+    float x[CH];
+    f32x4 v[CH];
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int s = s0 + i * G < used ? s0 + i * G : g;  // clamped; weight 0 below
+      x[i] = merge_ld1<COH>(ls + (int64_t)s * lse_stride);
+      v[i] = merge_ld4<COH>(ps + (int64_t)s * part_stride);
+    }
+    float cpeak = peak;
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const bool live = s0 + i * G < used && x[i] > -1.0e29f;
+      cpeak = live ? fmaxf(cpeak, x[i]) : cpeak;
+    }
+    const float keep = expf(peak - cpeak);
+    tot *= keep;
+    acc *= keep;
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const bool live = s0 + i * G < used && x[i] > -1.0e29f;
+      const float wgt = live ? expf(x[i] - cpeak) : 0.0f;
+      tot += wgt;
+      acc += live ? v[i] * wgt : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    peak = cpeak;
+  }
+}
+
+// One output row (b, h, q) of a wide merge by all kMergeThreads threads of
+// a workgroup (it holds two workgroup barriers): thread t = g (D / 4) + c
+// takes dims 4c .. 4c + 3 of group g's splits; speak, stot and sacc are
+// kMergeThreads entries of LDS each. MAXCH as in merge_one: with 8 the
+// caller never has more than 8 splits per group.
+template <bool BF16, int MAXCH = kMergeChunk, bool COH = false>
+__device__ __forceinline__ void merge_wide_row(const float* parts, const float* lse, void* out,
+                                               int sq, int heads, int dim, int slots, int used,
+                                               int b, int h, int q, int t, float* speak,
+                                               float* stot, f32x4* sacc) {
+  using E = Elem<BF16>;
+  const int d4n = dim / 4;
+  const int G = kMergeThreads / d4n;
+  const int c = t % d4n, g = t / d4n;
+  const bool act = g < G;
+  const int64_t base = ((int64_t)b * heads + h) * slots * sq + q;  // (b, h, split 0, q)
+  const float* ls = lse + base;
+  const float* ps = parts + base * dim + 4 * c;
+  const int64_t part_stride = (int64_t)sq * dim;
+  float peak = kNegBig, tot = 0.0f;
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (act) {
+    // The smallest chunk of 4, 8 or 16 that holds a group's splits (16
+    // beyond): 64 splits over 8 groups are one chunk of 8, not 16 with half
+    // of the loads clamped. The live splits are summed in the same order.
+    const int per = (used + G - 1) / G;
+    if (per <= 4)
+      wide_group<4, COH>(ls, ps, sq, part_stride, g, G, used, peak, tot, acc);
+    else if (MAXCH <= 8 || per <= 8)
+      wide_group<8, COH>(ls, ps, sq, part_stride, g, G, used, peak, tot, acc);
+    else
+      wide_group<kMergeChunk, COH>(ls, ps, sq, part_stride, g, G, used, peak, tot, acc);
+    if (c == 0) speak[g] = peak;  // the same in every thread of the group
+  }
+  __syncthreads();
+  float top = kNegBig;
+  for (int k = 0; k < G; ++k) top = fmaxf(top, speak[k]);
+  if (act) {
+    const float scale = expf(peak - top);  // 0 for an empty group below a live peak
+    sacc[t] = acc * scale;
+    if (c == 0) stot[g] = tot * scale;
+  }
+  __syncthreads();
+  if (g == 0) {
+    f32x4 a = {0.0f, 0.0f, 0.0f, 0.0f};
+    float total = 0.0f;
+    for (int k = 0; k < G; ++k) {
+      a += sacc[k * d4n + c];
+      total += stot[k];
+    }
+    const float inv = 1.0f / fmaxf(total, 1.0e-30f);
+    u32x2 w;
+    w.x = E::pack2(a[0] * inv, a[1] * inv);
+    w.y = E::pack2(a[2] * inv, a[3] * inv);
+    u16* dst = static_cast<u16*>(out) + (((int64_t)b * sq + q) * heads + h) * dim + 4 * c;
+    *reinterpret_cast<u32x2*>(dst) = w;
+  }
+  __syncthreads();  // the LDS entries may be written again
+}
+
+// Fused split merge of fgw_mha_fwd (FwdParams::arrivals set, mode 1, key
+// layout, at most kMergeChunk splits). Once a work item of task (b, h, q
+// tile) has written its partial rows and LSE, its workgroup counts itself in
+// at the task's counter; the one that arrives last (the task's `used` work
+// items counted) merges the task's rows into the output with the stand-alone
+// merge's arithmetic (merge_rows: one (row, 4 dims) per thread), so the
+// output has the bits of the two-launch call, and sets the counter back to
+// zero for the next call. Visibility across XCDs without any L2 write-back
+// or invalidation (a release of the whole L2 per work item measured slower
+// than the second launch it saves): the partial rows and LSE are
+// agent-scope atomic stores (store_row, coherent at the device), every wave
+// waits until its stores are complete before the count, the count is a
+// vector global atomic at agent scope, and the merge reads the partials with
+// agent-scope atomic loads (merge_ld1), issued after the count has returned.
+// Every thread of the workgroup calls it; it uses 4 bytes of `lds`.
+// MAXCH 8 (head-dim tile 32, whose kernels would lose a workgroup per CU to
+// the 16-split chunk's registers) leaves that chunk out; the planner then
+// fuses no plan that needs it (fused_merge_counters).
+// Counters per task in the arrival buffer: one 128-byte line each, so that
+// the atomics of different tasks do not queue on one line.
+constexpr int kArrivalStride = 32;
+template <int DPAD>
+constexpr int kFusedMergeMaxChunk = DPAD == 32 ? 8 : kMergeChunk;
+template <bool BF16, int THREADS, int ROWS_TILE, int MAXCH>
+__device__ void arrive_and_merge(const FwdParams& p, int b, int h, int qt, int used,
+                                 unsigned char* lds, int tid) {
+  static_assert(THREADS == kMergeThreads, "the merge runs on one kMergeThreads workgroup");
+  wait_vm<0>();     // this wave's partial rows and LSE are complete at the device
+  __syncthreads();  // ... and every wave's
+  int* flag = reinterpret_cast<int*>(lds);
+  int32_t* ctr = p.arrivals + (((int64_t)b * p.heads + h) * p.q_tiles + qt) * kArrivalStride;
+  if (tid == 0) {
+    const int prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *flag = prev == used - 1;
+  }
+  __syncthreads();
+  if (!*flag) return;  // uniform: another work item of the task arrives later
+  // The merge's inputs pass through opaque copies, so that the compiler
+  // keeps the address and chunk arithmetic derived from them here instead
+  // of hoisting it out of the work-item loop, where it would stay live
+  // across the main loop (and cost the kernel its second workgroup per CU).
+  int sq = p.sq, heads = p.heads, dim = p.dim, slots = p.splits;
+  asm volatile("" : "+s"(sq), "+s"(heads), "+s"(dim), "+s"(slots), "+s"(used), "+s"(b), "+s"(h),
+               "+s"(qt));
+  asm volatile("" : "+v"(tid));
+  const int q0 = qt * ROWS_TILE;
+  const int rows = sq - q0 < ROWS_TILE ? sq - q0 : ROWS_TILE;
+  merge_rows<BF16, MAXCH, true>(p.parts, p.lse, p.out, sq, heads, dim, slots, used, b, h, q0,
+                                rows, tid, kMergeThreads);
+  if (tid == 0) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Page id of the page holding logical position pos.
@@ -1005,10 +1293,18 @@ __global__ __launch_bounds__(C::THREADS) void fwd_kernel(FwdParams p,
           }
           store_row<C>(p, b, h, split, row, d0, acc, 1.0f / fmaxf(t2, 1.0e-30f));
           if (p.mode == 1 && d0 == 0) {
-            p.lse[(((int64_t)b * p.heads + h) * p.splits + split) * p.sq + row] = lse_of(mm, t2);
+            float* lp = p.lse + (((int64_t)b * p.heads + h) * p.splits + split) * p.sq + row;
+            if (p.arrivals != nullptr)
+              __hip_atomic_store(lp, lse_of(mm, t2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            else
+              *lp = lse_of(mm, t2);
           }
         }
       }
+    }
+    if (C::LAYOUT == kLayoutKey && p.mode == 1 && p.arrivals != nullptr) {
+      arrive_and_merge<C::BF16, C::THREADS, C::ROWS_TILE, kFusedMergeMaxChunk<C::DPAD>>(
+          p, b, h, qt, nsplit, smem, tid);
     }
   }
 }

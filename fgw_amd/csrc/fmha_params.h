@@ -49,6 +49,12 @@ struct FwdParams {
   // Tile-balanced plans in a whole call: a tile of one split writes its
   // normalised output rows directly (the merge skips them).
   int32_t split_direct;
+  // Fused split merge (mode 1, query and key layouts): one counter per task
+  // (b H + h) q_tiles + q tile, zero on entry; every work item counts itself
+  // in once its partial rows are written, the last one of a task merges the
+  // task's rows into `out` and sets the counter back to zero. nullptr: the
+  // merge is a separate launch.
+  int32_t* arrivals;
 };
 
 struct MergeParams {

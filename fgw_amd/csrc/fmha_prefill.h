@@ -29,13 +29,18 @@
 // M(n + 1)).
 //
 // DMA. Block j's K and V tiles go to K slot j % 4 and V slot j % 4; the
-// batch of block j (clamped to N - 1) is issued in phase 2(j - 2) by every
-// wave (its share of the tile's 1 KB instructions). Both slots held block
-// j - 4, last read in phase 2j - 7 (K) and 2j - 5 (V). The wait at the end
-// of phase 2m + 1 leaves only the batch of block m + 2 in flight, so block
-// m + 1 (K read from phase 2m + 2) has landed; V of block m was waited for
-// a pair earlier. The pool offset of block j comes from a 64-block window of
-// per-lane offsets (one table read per lane every 64 blocks) by readlane.
+// batch of block j < N is issued in phase 2(j - 2) by every wave (its share
+// of the tile's 1 KB instructions). Both slots held block j - 4, last read
+// in phase 2j - 7 (K) and 2j - 5 (V). The wait at the end of phase 2m + 1
+// leaves only the batch of block m + 2 in flight (none once m + 2 >= N), so
+// block m + 1 (K read from phase 2m + 2) has landed; V of block m was
+// waited for a pair earlier. The pool offset of block j comes from a
+// 64-block window of per-lane offsets (one table read per lane every 64
+// blocks) by readlane; the first window's page ids and Q are read before
+// the item's cache length arrives (guessing a full cache for the first key).
+// After M(N) no DMA is in flight and nothing reads the K ring: each wave
+// stages its output rows there right away (group A's during group B's
+// M(N)).
 // The loads are issued by inline assembly: the compiler then neither sees
 // them as LDS writes (it would otherwise wait for every outstanding DMA
 // before each transposing LDS read) nor counts them; the explicit waits here
@@ -101,23 +106,40 @@ struct PCfg {
   static_assert(LDS_BYTES <= kLdsBudget, "LDS budget of one CU");
 };
 
+// Page id of the page holding the first key of block j of a work item
+// (keys key0 + j BN ..), clamped to the table: the read does not depend on
+// len, so it can be issued before len is known. Evaluated per lane.
+template <class C>
+__device__ __forceinline__ int32_t block_page_id(const FwdParams& p, const int32_t* table_b,
+                                                 int key0, int j) {
+  const u32 pg = div_page((u32)key0 + (u32)j * C::BN, p.page_magic, p.page_shift);
+  const u32 last = (u32)p.width - 1u;
+  return table_b[pg < last ? pg : last];
+}
+
 // Pool byte offset (row * row_bytes) of the first key row of block j of a
-// work item (keys key0 + j BN ..), or -1 when the block needs the per-key
-// path (it straddles a page or len, leaves the pool, or D < DPAD). Blocks
-// j >= N are never loaded and read -1. Evaluated per lane, one block per lane.
+// work item, from the page id of its first key (block_page_id), or -1 when
+// the block needs the per-key path (it straddles a page or len, leaves the
+// pool, or D < DPAD). Blocks j >= N are never loaded and read -1.
+template <class C>
+__device__ __forceinline__ int64_t block_offset_of(const FwdParams& p, int32_t id,
+                                                   int64_t row_bytes, int key0, int N, int len,
+                                                   int j) {
+  const u32 page = (u32)p.page_size;
+  const u32 pos0 = (u32)key0 + (u32)j * C::BN;
+  const u32 pg0 = div_page(pos0, p.page_magic, p.page_shift);
+  const u32 off0 = pos0 - pg0 * page;
+  const int64_t row0 = (int64_t)id * page + off0;
+  const bool fast = j < N && off0 + C::BN <= page && (int64_t)pos0 + C::BN <= len && row0 >= 0 &&
+                    row0 + C::BN <= p.pool_rows && p.dim == C::DPAD;
+  return fast ? row0 * row_bytes : -1;
+}
+
 template <class C>
 __device__ __forceinline__ int64_t block_offset(const FwdParams& p, const int32_t* table_b,
                                                 int64_t row_bytes, int key0, int N, int len,
                                                 int j) {
-  const u32 page = (u32)p.page_size;
-  const int pos0 = key0 + j * C::BN;
-  const bool live = j < N;
-  const u32 pg0 = live ? div_page((u32)pos0, p.page_magic, p.page_shift) : 0u;
-  const u32 off0 = (u32)pos0 - pg0 * page;
-  const int64_t row0 = (int64_t)table_b[pg0] * page + off0;
-  const bool fast = live && off0 + C::BN <= page && pos0 + C::BN <= len && row0 >= 0 &&
-                    row0 + C::BN <= p.pool_rows && p.dim == C::DPAD;
-  return fast ? row0 * row_bytes : -1;
+  return block_offset_of<C>(p, block_page_id<C>(p, table_b, key0, j), row_bytes, key0, N, len, j);
 }
 
 // Offsets of blocks [64 w, 64 w + 64) of a work item, one per lane (lane l:
@@ -290,15 +312,25 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p,
   const DmaLanes<C> dl(lane, wave, row_bytes);
   const BlockDma<C> bd(dl, wave, row_bytes);
 
+  // Work items: the programs of one XCD (hardware: workgroup i runs on XCD
+  // i % 8) share one contiguous range of the items, interleaved: program
+  // `local` of the XCD takes items a + local, a + local + nx, ... So at any
+  // time the XCD's CUs work on neighbouring items (the query tiles of one
+  // (b, h)), whose K/V its L2 then holds once. With one item per program
+  // this is the plain contiguous assignment.
   const int grid = gridDim.x;
-  const int prog = xcd_remap(blockIdx.x, grid);
+  const int xcd = (int)blockIdx.x % kNumXcd, local = (int)blockIdx.x / kNumXcd;
+  const int q8 = grid / kNumXcd, r8 = grid % kNumXcd;
+  const int nx = q8 + (xcd < r8 ? 1 : 0);           // programs on this XCD
+  const int sx = xcd * q8 + (xcd < r8 ? xcd : r8);  // first of them in program order
   const int per = p.work / grid, rem = p.work % grid;
-  const int first = prog * per + (prog < rem ? prog : rem);
-  const int count = per + (prog < rem ? 1 : 0);
+  const int a = sx * per + (sx < rem ? sx : rem);
+  const int end = (sx + nx) * per + (sx + nx < rem ? sx + nx : rem);
+  const int count = local < end - a ? (end - a - local + nx - 1) / nx : 0;
   const int capacity = p.width * p.page_size;
 
   for (int it = 0; it < count; ++it) {
-    int w = first + it;
+    int w = a + local + nx * it;
     int split, nsplit = p.splits, qt, h, b;
     if (p.split_keys > 0) {
       // Tile-balanced causal plan: the items of one (b, h) are contiguous
@@ -333,11 +365,38 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p,
     const int32_t* table_b = table + (int64_t)b * p.width;
     const char* kb = static_cast<const char*>(p.k) + (int64_t)h * p.dim * 2;
     const char* vb = static_cast<const char*>(p.v) + (int64_t)h * p.dim * 2;
+    const int q0 = qt * C::ROWS_TILE;
+    const int row_base = q0 + wave * C::ROWS_WAVE;
+    const int qrow = row_base + il;
+
+    const int tile_last = (q0 + C::ROWS_TILE < p.sq ? q0 + C::ROWS_TILE : p.sq) - 1;
+    // The item's first key block, given its cache length.
+    auto first_block = [&](int n) {
+      int mv = p.causal ? n - p.sq + tile_last + 1 : n;
+      mv = mv < 0 ? 0 : (mv > n ? n : mv);
+      return (int)((int64_t)((mv + C::BN - 1) / C::BN) * split / nsplit);
+    };
+    // Issued before len is known, so that the round trips overlap: the page
+    // ids of the first 64-block window for a full cache (read again below if
+    // len moves the item's first key; split 0 always starts at key 0), then
+    // Q^T (B of the QK^T product).
+    const int key0_full = first_block(capacity) * C::BN;
+    int32_t id_first = block_page_id<C>(p, table_b, key0_full, lane);
+    u32x4 qf[C::KK];
+    {
+      const u16* qp =
+          static_cast<const u16*>(p.q) + (((int64_t)b * p.sq + qrow) * p.heads + h) * p.dim;
+#pragma unroll
+      for (int kk = 0; kk < C::KK; ++kk) {
+        const int d = 16 * kk + 8 * hh;
+        u32x4 val = {0u, 0u, 0u, 0u};
+        if (qrow < p.sq && d < p.dim) val = load16(qp + d);
+        qf[kk] = val;
+      }
+    }
 
     int len = lengths[b];
     len = len < 0 ? 0 : (len > capacity ? capacity : len);
-    const int q0 = qt * C::ROWS_TILE;
-    const int tile_last = (q0 + C::ROWS_TILE < p.sq ? q0 + C::ROWS_TILE : p.sq) - 1;
     int max_vis = p.causal ? len - p.sq + tile_last + 1 : len;
     max_vis = max_vis < 0 ? 0 : (max_vis > len ? len : max_vis);
     const int nblk = (max_vis + C::BN - 1) / C::BN;
@@ -348,10 +407,8 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p,
 
     // Rows of this wave and their visible key counts; blocks that end above
     // wmin hold keys some row of the wave cannot see and are masked.
-    const int row_base = q0 + wave * C::ROWS_WAVE;
     int wmin = p.causal ? len - p.sq + row_base + 1 : len;
     wmin = wmin < 0 ? 0 : (wmin > len ? len : wmin);
-    const int qrow = row_base + il;
     int vis = p.causal ? len - p.sq + qrow + 1 : len;
     vis = vis < 0 ? 0 : (vis > len ? len : vis);
 
@@ -362,52 +419,98 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p,
 #pragma unroll
       for (int v = 0; v < 16; ++v) o[dt][v] = 0.0f;
 
-    __syncthreads();  // the previous work item no longer reads the rings
+    // Output of this wave's rows: O/l of the work item, or the partial
+    // (O/l, LSE) of its split. With D == DPAD the rows go out through LDS,
+    // each wave through its own 32 * kStagedRowBytes bytes from the start of
+    // the rings; the caller guarantees that no DMA writes and no wave reads
+    // that region meanwhile. kStageInK: the eight regions lie in the K ring
+    // (head-dim tile 128; at 64 the upper four reach into the V ring).
+    constexpr bool kStageInK = C::WAVES * 32 * kStagedRowBytes<C> <= C::NKSLOT * C::TILE_BYTES;
+    // Partials, unless a one-split tile of a tile-balanced whole call writes
+    // its output rows directly.
+    const bool to_parts = p.mode == 1 && !(p.split_direct && nsplit == 1);
+    auto store_output = [&]() {
+      const float tot = pair_sum(l);
+      if (p.dim == C::DPAD) {
+        static_assert(C::WAVES * 32 * kStagedRowBytes<C> <= C::LDS_BYTES, "staged rows fit");
+        const bool f32 = to_parts;
+        float* fdst =
+            f32 ? p.parts + ((((int64_t)b * p.heads + h) * p.splits + split) * p.sq + row_base) *
+                                C::DPAD
+                : nullptr;
+        unsigned char* bdst =
+            f32 ? nullptr
+                : static_cast<unsigned char*>(p.out) +
+                      (((int64_t)b * p.sq + row_base) * p.heads + h) * C::DPAD * 2;
+        store_rows_staged<C>(smem + wave * 32 * kStagedRowBytes<C>, lane, o,
+                             1.0f / fmaxf(tot, 1.0e-30f), f32, fdst, bdst,
+                             (int64_t)p.heads * C::DPAD * 2, p.sq - row_base);
+        if (to_parts && hh == 0 && qrow < p.sq)
+          p.lse[(((int64_t)b * p.heads + h) * p.splits + split) * p.sq + qrow] = lse_of(m, tot);
+      } else if (qrow < p.sq) {
+        const float inv = 1.0f / fmaxf(tot, 1.0e-30f);
+#pragma unroll
+        for (int dt = 0; dt < C::DT; ++dt)
+#pragma unroll
+          for (int gq = 0; gq < 4; ++gq) {
+            const int d0 = 32 * dt + 8 * gq + 4 * hh;
+            if (d0 < p.dim) {
+              f32x4 val = {o[dt][4 * gq], o[dt][4 * gq + 1], o[dt][4 * gq + 2], o[dt][4 * gq + 3]};
+              store_row<C>(p, b, h, split, qrow, d0, val, inv, -1, 0, to_parts ? 1 : 0);
+            }
+          }
+        if (to_parts && hh == 0) {
+          p.lse[(((int64_t)b * p.heads + h) * p.splits + split) * p.sq + qrow] = lse_of(m, tot);
+        }
+      }
+    };
+
+    __syncthreads();  // the previous work item no longer reads or stages in the rings
 
     if (N > 0) {
       // Window of 64 block offsets holding the next batch's block; the
       // following window is read one window ahead.
-      BlockWindow win0{0, block_offset<C>(p, table_b, row_bytes, key0, N, len, lane)};
+      // Each branch consumes its own page-id load, so the common one (the
+      // guess held) waits only for that load and not for Q behind it.
+      BlockWindow win0{0, 0};
+      if (key0 == key0_full)
+        win0.off = block_offset_of<C>(p, id_first, row_bytes, key0, N, len, lane);
+      else
+        win0.off = block_offset<C>(p, table_b, row_bytes, key0, N, len, lane);
       BlockWindow win1{1, 0};
-      // K and V of block j (clamped to N - 1) into K slot j % 4, V slot j % 4.
+      // K and V of block j < N into K slot j % 4, V slot j % 4.
       auto issue_block = [&](int j) {
-        const int jc = j < N ? j : N - 1;
-        if ((jc >> 6) != win0.w) {  // uniform: the block entered the next window
+        if ((j >> 6) != win0.w) {  // uniform: the block entered the next window
           win0 = win1;
           win1 = BlockWindow{win0.w + 1, block_offset<C>(p, table_b, row_bytes, key0, N, len,
                                                          64 * (win0.w + 1) + lane)};
         }
-        const int64_t off = readlane64(win0.off, jc & 63);
+        const int64_t off = readlane64(win0.off, j & 63);
         const u32 kdst = kring_lds + (u32)((j % C::NKSLOT) * C::TILE_BYTES);
         const u32 vdst = vring_lds + (u32)((j % C::NVSLOT) * C::TILE_BYTES);
         if (off >= 0) {
           issue_fast_block<C>(kb + off, vb + off, kdst, vdst, bd, wave);
         } else {
-          issue_slow_tile<C, false>(p, table_b, kb, row_bytes, key0 + jc * C::BN, len, kdst, wave,
+          issue_slow_tile<C, false>(p, table_b, kb, row_bytes, key0 + j * C::BN, len, kdst, wave,
                                     lane);
-          issue_slow_tile<C, true>(p, table_b, vb, row_bytes, key0 + jc * C::BN, len, vdst, wave,
+          issue_slow_tile<C, true>(p, table_b, vb, row_bytes, key0 + j * C::BN, len, vdst, wave,
                                    lane);
         }
       };
+      // Wait until block j has landed, the batch of block j + 1 (issued
+      // after it when j + 1 < N) possibly still in flight.
+      auto wait_block = [&](int j) {
+        if (j + 1 < N)
+          wait_vm<C::BATCH>();
+        else
+          wait_vm<0>();
+      };
       issue_block(0);
-      issue_block(1);
+      if (1 < N) issue_block(1);
 
-      // Q^T operands (B of the QK^T product) load while the first blocks land.
-      u32x4 qf[C::KK];
-      {
-        const u16* qp =
-            static_cast<const u16*>(p.q) + (((int64_t)b * p.sq + qrow) * p.heads + h) * p.dim;
-#pragma unroll
-        for (int kk = 0; kk < C::KK; ++kk) {
-          const int d = 16 * kk + 8 * hh;
-          u32x4 val = {0u, 0u, 0u, 0u};
-          if (qrow < p.sq && d < p.dim) val = load16(qp + d);
-          qf[kk] = val;
-        }
-      }
       win1.off = block_offset<C>(p, table_b, row_bytes, key0, N, len, 64 + lane);
-      wait_vm<C::BATCH>();  // block 0
-      // Q has landed too (its loads are younger than block 0's). The empty
+      wait_block(0);
+      // Q has landed too (its loads are older than block 0's). The empty
       // assembly makes the compiler wait for them here, once, instead of
       // before the first QK^T MFMA of every matrix phase, where its vmcnt(0)
       // would also wait for the DMA batch in flight.
@@ -436,92 +539,56 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p,
       };
       // Group A: M(n) in phase 2n, S(n) in phase 2n + 1. Group B: S(n - 1)
       // in phase 2n, M(n) in phase 2n + 1. Every wave issues its share of
-      // block n + 2 at the start of phase 2n and, at the end of phase
-      // 2n + 1, waits until only that batch may be in flight (block n + 1
-      // has landed). Straight-line loops per group keep the register
-      // assignment of O, S and P fixed across phases; each group passes
-      // 2N + 2 barriers.
+      // block n + 2 (when it exists) at the start of phase 2n and, at the
+      // end of phase 2n + 1, waits until block n + 1 has landed. After the
+      // barrier that ends phase 2N - 1 no DMA is in flight and no wave reads
+      // the K ring any more (M(N) reads V only): each wave then stages its
+      // output rows in its region of the K ring right after its last matrix
+      // phase, group A's during group B's M(N) (when the regions lie in the
+      // K ring; else after one more barrier). Straight-line loops per group
+      // keep the register assignment of O, S and P fixed across phases; both
+      // groups pass the same number of barriers.
       if (group_a) {
-        issue_block(2);
+        if (2 < N) issue_block(2);
         mphase(0, off, on);
         __syncthreads();
         sphase(0);
-        wait_vm<C::BATCH>();
+        wait_block(1);
         __syncthreads();
         for (int n = 1; n < N; ++n) {
-          issue_block(n + 2);
+          if (n + 2 < N) issue_block(n + 2);
           mphase(n, on, on);
           __syncthreads();
           sphase(n);
-          wait_vm<C::BATCH>();
+          wait_block(n + 1);
           __syncthreads();
         }
-        issue_block(N + 2);
         mphase(N, on, off);
         __syncthreads();
-        wait_vm<C::BATCH>();
-        __syncthreads();
+        if constexpr (!kStageInK) __syncthreads();  // group B no longer reads the V ring
+        store_output();
       } else {
-        issue_block(2);
+        if (2 < N) issue_block(2);
         __syncthreads();
         mphase(0, off, on);
-        wait_vm<C::BATCH>();
+        wait_block(1);
         __syncthreads();
         for (int n = 1; n < N; ++n) {
-          issue_block(n + 2);
+          if (n + 2 < N) issue_block(n + 2);
           sphase(n - 1);
           __syncthreads();
           mphase(n, on, on);
-          wait_vm<C::BATCH>();
+          wait_block(n + 1);
           __syncthreads();
         }
-        issue_block(N + 2);
         sphase(N - 1);
         __syncthreads();
         mphase(N, on, off);
-        wait_vm<C::BATCH>();
-        __syncthreads();
+        if constexpr (!kStageInK) __syncthreads();  // every wave's V reads are done
+        store_output();
       }
-      wait_vm<0>();  // no DMA of this work item outlives it
-    }
-
-    const float tot = pair_sum(l);
-    // Partials, unless a one-split tile of a tile-balanced whole call writes
-    // its output rows directly.
-    const bool to_parts = p.mode == 1 && !(p.split_direct && nsplit == 1);
-    if (p.dim == C::DPAD) {
-      // Every wave's DMA into the rings has landed (each waited for its own
-      // above) and no wave reads them any more: the rings stage the output.
-      __syncthreads();
-      static_assert(C::WAVES * 32 * kStagedRowBytes<C> <= C::LDS_BYTES, "staged rows fit the rings");
-      const bool f32 = to_parts;
-      float* fdst =
-          f32 ? p.parts + ((((int64_t)b * p.heads + h) * p.splits + split) * p.sq + row_base) *
-                              C::DPAD
-              : nullptr;
-      unsigned char* bdst = f32 ? nullptr
-                                : static_cast<unsigned char*>(p.out) +
-                                      (((int64_t)b * p.sq + row_base) * p.heads + h) * C::DPAD * 2;
-      store_rows_staged<C>(smem + wave * 32 * kStagedRowBytes<C>, lane, o,
-                           1.0f / fmaxf(tot, 1.0e-30f), f32, fdst, bdst,
-                           (int64_t)p.heads * C::DPAD * 2, p.sq - row_base);
-      if (to_parts && hh == 0 && qrow < p.sq)
-        p.lse[(((int64_t)b * p.heads + h) * p.splits + split) * p.sq + qrow] = lse_of(m, tot);
-    } else if (qrow < p.sq) {
-      const float inv = 1.0f / fmaxf(tot, 1.0e-30f);
-#pragma unroll
-      for (int dt = 0; dt < C::DT; ++dt)
-#pragma unroll
-        for (int gq = 0; gq < 4; ++gq) {
-          const int d0 = 32 * dt + 8 * gq + 4 * hh;
-          if (d0 < p.dim) {
-            f32x4 val = {o[dt][4 * gq], o[dt][4 * gq + 1], o[dt][4 * gq + 2], o[dt][4 * gq + 3]};
-            store_row<C>(p, b, h, split, qrow, d0, val, inv, -1, 0, to_parts ? 1 : 0);
-          }
-        }
-      if (to_parts && hh == 0) {
-        p.lse[(((int64_t)b * p.heads + h) * p.splits + split) * p.sq + qrow] = lse_of(m, tot);
-      }
+    } else {
+      store_output();
     }
   }
 }

@@ -18,6 +18,8 @@
 #include <torch/csrc/autograd/python_variable.h>
 
 #include <cstring>
+#include <map>
+#include <utility>
 
 #include "../../include/fgw_mha.h"
 
@@ -97,6 +99,25 @@ int launcher_init(Launcher* self, PyObject* args, PyObject* kwds) {
   return 0;
 }
 
+// Arrival counters of the fused split merge (fgw_mha_tensors.arrivals), one
+// zeroed int32 buffer per (device, stream), grown as plans need more. Every
+// completed call leaves its counters at zero, so calls in stream order share
+// the buffer, and calls on other streams (which may overlap) use their own.
+// While the stream is being captured into a graph the call merges in a
+// second launch instead: a replay may run on any stream. The buffers live
+// until the process ends (the map is never destroyed, so no device memory is
+// released after the runtime has shut down).
+int32_t* arrival_counters(int device, hipStream_t stream, int64_t need) {
+  hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &status) != hipSuccess || status != hipStreamCaptureStatusNone)
+    return nullptr;
+  static auto* buffers = new std::map<std::pair<int, uintptr_t>, at::Tensor>();
+  at::Tensor& buf = (*buffers)[{device, reinterpret_cast<uintptr_t>(stream)}];
+  if (!buf.defined() || buf.numel() < need)
+    buf = at::zeros({need}, at::TensorOptions().device(c10::kCUDA, device).dtype(at::kInt));
+  return static_cast<int32_t*>(buf.data_ptr());
+}
+
 // The checks of one call, in the order and with the messages of the Python
 // operator (shape, then dtype, then int32 metadata, then device/layout).
 PyObject* check_detail(const Launcher* self, const at::Tensor* x) {
@@ -150,12 +171,15 @@ PyObject* launcher_call(PyObject* obj, PyObject* args, PyObject* kwargs) {
     t.out = out.data_ptr();
     t.parts = nullptr;
     t.lse = nullptr;
+    t.arrivals = nullptr;
     if (self->ws_floats > 0) {
       ws = at::empty({self->ws_floats}, on_device.dtype(at::kFloat));
       t.parts = static_cast<float*>(ws.data_ptr());
       t.lse = t.parts + self->plan.parts_floats;
     }
     const hipStream_t stream = c10::hip::getCurrentHIPStream(self->device).stream();
+    if (self->plan.arrival_counters > 0)
+      t.arrivals = arrival_counters(self->device, stream, self->plan.arrival_counters);
     const int rc = self->fwd(&self->shape, &self->plan, &t, stream);
     if (rc != FGW_MHA_OK) {
       PyErr_SetString(rc == FGW_MHA_EHIP ? PyExc_RuntimeError : PyExc_ValueError,

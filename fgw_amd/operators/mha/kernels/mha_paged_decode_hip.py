@@ -124,6 +124,12 @@ class _Launch(_launch.Launcher):
             if plan.split_keys else "even"
         self.query_tile_tasks = plan.query_tile_tasks
         self.execution_mode = "split_and_merge" if plan.execution_mode else "direct_single_split"
+        # True: a call merges the splits inside the partial kernel (the last
+        # work item of each task merges it; one launch, with per-stream
+        # arrival counters), except while its stream is captured into a
+        # graph, where the merge is a second launch. The output bits are the
+        # same either way; partial_kernel / merge_kernel stay separate.
+        self.merge_fused = plan.arrival_counters > 0
         self.execution_path = ROUTE
         self.layout = _LAYOUT_NAMES[plan.layout]
         self.dim_padded = plan.dim_padded

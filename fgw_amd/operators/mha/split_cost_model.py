@@ -102,17 +102,17 @@ def planner_takes_prefill(batch, sq, heads, dim, num_cus, wg_per_cu, kv_tokens) 
 def single_stage_splits(batch, sq, heads, dim, capacity_tokens, splits, num_cus,
                         wg_per_cu_key_single) -> int:
     """fgw_mha_plan's single_stage_splits (fmha_api.hip) restated: a short
-    decode plan (Sq <= 4, key layout, head-dim tile 128) of >= 16 even splits
-    that gives each CU at most one work item moves to the single-stage key
-    kernel with 4x the splits (>= 512 keys each), else 2x (>= 256 keys);
-    returns that split count, or 0 to keep the plan."""
+    decode plan (Sq <= 16, key layout, head-dim tile 128) of >= 16 even
+    splits that gives each CU at most one work item moves to the single-stage
+    key kernel with 4x the splits (Sq <= 4, >= 512 keys each), else 2x
+    (>= 256 keys); returns that split count, or 0 to keep the plan."""
     dpad = 32
     while dpad < dim:
         dpad *= 2
-    if (dpad != 128 or sq > 4 or splits < 16 or wg_per_cu_key_single < 2
+    if (dpad != 128 or sq > 16 or splits < 16 or wg_per_cu_key_single < 2
             or batch * heads * splits > num_cus):
         return 0
-    if 4 * splits <= SPLITS[-1] and capacity_tokens // (4 * splits) >= 512:
+    if sq <= 4 and 4 * splits <= SPLITS[-1] and capacity_tokens // (4 * splits) >= 512:
         return 4 * splits
     if 2 * splits <= SPLITS[-1] and capacity_tokens // (2 * splits) >= 256:
         return 2 * splits

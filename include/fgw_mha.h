@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define FGW_MHA_ABI_VERSION 5
+#define FGW_MHA_ABI_VERSION 6
 
 typedef enum {
   FGW_MHA_OK = 0,
@@ -134,6 +134,12 @@ typedef struct {
                               for s < clamp(ceil(len_b / split_keys), 1, num_splits) */
   int32_t stages;          /* K/V stages per key group of the selected kernel (query and key
                               layouts; the prefill layout's rings have 4 slots: 4) */
+  int32_t arrival_counters; /* > 0: fgw_mha_fwd can fuse this split plan's merge into the
+                              partial kernel when the call supplies an arrival buffer of this
+                              many int32 (fgw_mha_tensors.arrivals; one 128-byte counter line
+                              per query-tile task: 32 x query_tile_tasks); 0: the merge is
+                              always a second launch (direct plans, the query and prefill
+                              layouts, and tasks whose merge takes more than two rounds) */
 } fgw_mha_plan_t;
 
 /* Device buffers of one call. Workspaces are owned by the caller and sized
@@ -147,6 +153,12 @@ typedef struct {
   void* out;
   float* parts; /* [B, H, S, Sq, D] */
   float* lse;   /* [B, H, S, Sq]    natural-log sum-exp, -1e30 for an empty split */
+  int32_t* arrivals; /* NULL, or plan.arrival_counters int32, all zero on entry, for
+                        fgw_mha_fwd's fused merge: each task's last work item merges the
+                        task's rows and returns its counter to zero, so the buffer is zero
+                        again when the call completes and can serve the next call on the
+                        same stream. Calls that overlap (other streams) need their own
+                        counters. Ignored by the other entry points. */
 } fgw_mha_tensors;
 
 /* ABI version of the loaded library (FGW_MHA_ABI_VERSION). No reference
@@ -176,14 +188,22 @@ int fgw_mha_plan(const fgw_mha_shape* shape, const fgw_mha_request* request,
                  const fgw_mha_device_info* device, fgw_mha_plan_t* plan);
 
 /* Full forward: the direct kernel with the fused normalise/cast/store
- * epilogue when num_splits == 1, else partial + merge. Replaces the compiled
- * launch callable returned by build_kernel (v7.py:471-473, :495-498). */
+ * epilogue when num_splits == 1, else partial + merge: one launch when the
+ * plan has arrival_counters and t->arrivals is set (the last work item of
+ * each (b, h, q tile) merges its splits, with the same arithmetic and so the
+ * same output bits as the separate merge), two launches otherwise. Replaces
+ * the compiled launch callable returned by build_kernel (v7.py:471-473,
+ * :495-498; the reference always launches its merge separately,
+ * v7.py:488-493). */
 int fgw_mha_fwd(const fgw_mha_shape* shape, const fgw_mha_plan_t* plan,
                 const fgw_mha_tensors* t, hipStream_t stream);
 
 /* Bytes of the static device scratch that fgw_mha_fwd_noalloc uses as its
  * split workspace (partials then LSE, parts_floats + lse_floats fp32). */
 #define FGW_MHA_NOALLOC_SCRATCH_BYTES (32ll << 20)
+/* Its static arrival buffer (int32): plans whose arrival_counters fit fuse
+ * their merge there, larger ones merge in a second launch. */
+#define FGW_MHA_NOALLOC_ARRIVALS 65536
 
 /* fgw_mha_fwd without a caller workspace and without any allocation: the
  * split workspace (t->parts / t->lse are ignored and may be NULL) is a static
@@ -193,10 +213,13 @@ int fgw_mha_fwd(const fgw_mha_shape* shape, const fgw_mha_plan_t* plan,
  * for callers that cannot allocate device memory (HIP graph capture, serving
  * loops, harnesses that forbid hipMalloc). Plans whose parts_floats +
  * lse_floats exceed the scratch are rejected (FGW_MHA_EUNSUPPORTED). Direct
- * plans (num_splits == 1) need no scratch. Every call on one GPU shares that
- * GPU's scratch: calls that overlap on one GPU (other streams, other host
- * threads) race on it. Nothing in it needs clearing: the partial kernel
- * writes every row the merge reads. */
+ * plans (num_splits == 1) need no scratch. Plans with arrival_counters (up
+ * to FGW_MHA_NOALLOC_ARRIVALS) fuse their merge, with static counters that
+ * every completed call leaves at zero (t->arrivals is ignored). Every call on
+ * one GPU shares that GPU's scratch and counters: calls that overlap on one
+ * GPU (other streams, other host threads) race on them. Nothing in the
+ * scratch needs clearing: the partial kernel writes every row the merge
+ * reads. */
 int fgw_mha_fwd_noalloc(const fgw_mha_shape* shape, const fgw_mha_plan_t* plan,
                         const fgw_mha_tensors* t, hipStream_t stream);
 

@@ -68,7 +68,7 @@ def test_single_stage_rule_matches_the_planner(lib):
     moved = 0
     for b in (1, 2, 4, 16):
         for h in (1, 4, 8, 32):
-            for sq in (1, 4, 5, 16):
+            for sq in (1, 4, 5, 16, 17):
                 for d in (64, 128):
                     for kv in (1024, 4096, 8192, 32768, 65536):
                         s = shape(b=b, h=h, sq=sq, d=d, kv=kv)
@@ -384,3 +384,33 @@ def test_cost_model_with_an_explicit_layout_keeps_that_layout(lib, monkeypatch):
     pre = K.build_kernel(2, sq, 8, 128, 2 * kv, kv // 128, 128, False, "bfloat16", 0,
                          split_policy="cost_model", full_kv_cache=True, layout="prefill")
     assert pre.layout == "prefill"
+
+
+def test_plan_fused_merge_counters(lib):
+    """arrival_counters: the split plans whose merge fgw_mha_fwd fuses (key
+    layout, Sq <= 2, at most 16 splits; at most 8 at head-dim tile 32) carry
+    one 128-byte counter line (32 int32) per task; others carry none."""
+    def plan(req, **kw):
+        return _lib.plan(shape(**kw), req, DEVICE)
+    key, line = _lib.LAYOUT_KEY, 32
+    assert plan(_lib.Request(16, -1, key)).arrival_counters == 16 * line  # B2 H8 Q1
+    assert plan(_lib.Request(8, -1, key), sq=2).arrival_counters == 16 * line
+    assert plan(_lib.Request(1, -1, key)).arrival_counters == 0
+    assert plan(_lib.Request(32, -1, key)).arrival_counters == 0
+    assert plan(_lib.Request(8, -1, key), sq=3).arrival_counters == 0
+    assert plan(_lib.Request(8, -1, key), d=32).arrival_counters == 16 * line
+    assert plan(_lib.Request(16, -1, key), d=32).arrival_counters == 0
+    assert plan(_lib.Request(16, -1, key), d=64).arrival_counters == 16 * line
+    assert plan(_lib.Request(4, -1, _lib.LAYOUT_QUERY), sq=2).arrival_counters == 0
+    assert plan(_lib.Request(4, -1, _lib.LAYOUT_PREFILL), sq=4096, kv=2048).arrival_counters == 0
+
+
+def test_fwd_rejects_a_plan_with_other_arrival_counters(lib):
+    sh = shape(b=2, sq=1, h=8, d=128, kv=8192)
+    p = _lib.plan(sh, _lib.Request(16, -1, _lib.LAYOUT_KEY), DEVICE)
+    assert p.arrival_counters == 16 * 32
+    p.arrival_counters = 16
+    t = _lib.Tensors()
+    rc = lib.fgw_mha_fwd(ctypes.byref(sh), ctypes.byref(p), ctypes.byref(t), None)
+    assert rc == _lib.FGW_MHA_EINVAL
+    assert b"plan does not match" in lib.fgw_mha_last_error()

@@ -128,7 +128,8 @@ def test_single_stage_splits_known_answers():
     # kernel, 0 = keep the plan; 256 CUs, two single-stage programs per CU.
     cases = [((2, 1, 8, 128, 32768, 16), 64), ((1, 1, 8, 128, 32768, 32), 64),
              ((2, 1, 8, 128, 8192, 16), 32), ((2, 4, 8, 128, 65536, 16), 64),
-             ((2, 16, 8, 128, 32768, 16), 0), ((4, 1, 8, 128, 32768, 8), 0),
+             ((2, 16, 8, 128, 32768, 16), 32), ((2, 8, 8, 128, 8192, 16), 32),
+             ((2, 17, 8, 128, 32768, 16), 0), ((4, 1, 8, 128, 32768, 8), 0),
              ((2, 1, 8, 64, 32768, 16), 0), ((4, 1, 8, 128, 32768, 16), 0),
              ((1, 1, 1, 128, 4096, 64), 0), ((2, 1, 8, 128, 4096, 16), 0)]
     for args, want in cases:
