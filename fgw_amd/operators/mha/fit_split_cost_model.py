@@ -18,7 +18,11 @@ selection quality (least squares alone leaves it at zero; see fit()).
     python -m fgw_amd.operators.mha.fit_split_cost_model SCAN.jsonl [SCAN2.jsonl ...]
 
 writes split_cost_model.json beside split_cost_model.py and prints the
-in-sample evaluation (selected split's latency / best measured latency).
+in-sample evaluation (selected split's latency / best measured latency), the
+same figures for the C planner's own fill rule (fgw_mha_plan with
+num_splits = 0, read from the same records: the baseline the model must
+beat), and a held-out check: weights fitted without the --holdout suites,
+evaluated on them.
 """
 from __future__ import annotations
 
@@ -36,12 +40,30 @@ from scipy.optimize import nnls
 from fgw_amd.operators.mha import split_cost_model as M
 
 SUITES = ("decode-scan", "decode-batch", "decode-imbalanced", "grid")
+HOLDOUT = ("decode-batch", "decode-imbalanced")
 
 
 class _Device:
-    def __init__(self, num_cus, wg_per_cu):
+    def __init__(self, num_cus, wg_per_cu, wg_per_cu_key_single=2):
         self.num_cus = num_cus
         self.wg_per_cu = tuple(wg_per_cu)
+        self.wg_per_cu_key_single = wg_per_cu_key_single
+
+
+def fill_rule_splits(case, device) -> int:
+    """The C planner's automatic split count for a case (fgw_mha_plan with
+    num_splits = 0, its automatic layout), on the double-stage key kernel the
+    scans' explicit records ran on."""
+    import ctypes
+
+    from fgw_amd import _lib
+    dev = _lib.DeviceInfo(device.num_cus, (ctypes.c_int32 * _lib.NUM_LAYOUTS)(*device.wg_per_cu),
+                          1, device.wg_per_cu_key_single)
+    width = -(-case["capacity"] // 128)
+    shape = _lib.Shape(case["batch"], case["sq"], case["heads"], case["dim"],
+                       case["batch"] * width * 128, width, 128, 0, _lib.DTYPE_BFLOAT16)
+    stages = 2 if case["sq"] <= 32 and case["dim"] == 128 else 0
+    return _lib.plan(shape, _lib.Request(0, -1, -1, 0, stages), dev).num_splits
 
 
 def load_cases(paths) -> tuple:
@@ -52,7 +74,7 @@ def load_cases(paths) -> tuple:
         for line in pathlib.Path(path).read_text().splitlines():
             rec = json.loads(line)
             if rec["suite"] == "device":
-                dev = (rec["num_cus"], tuple(rec["wg_per_cu"]))
+                dev = (rec["num_cus"], tuple(rec["wg_per_cu"]), rec.get("wg_per_cu_key_single", 2))
                 if device is not None and device != dev:
                     raise ValueError("scan files come from different devices")
                 device = dev
@@ -65,15 +87,22 @@ def load_cases(paths) -> tuple:
             lengths = tuple(rec.get("lengths") or [rec["kv_len"]] * batch)
             key = (rec["suite"], rec["dtype"], batch, heads, dim, rec["q_len"], rec["kv_len"],
                    lengths)
-            case = cases.setdefault(key, {"batch": batch, "heads": heads, "dim": dim,
-                                          "sq": rec["q_len"], "capacity": rec["kv_len"],
-                                          "lengths": lengths, "lat": {}, "legacy": None})
+            case = cases.setdefault(key, {"suite": rec["suite"], "batch": batch, "heads": heads,
+                                          "dim": dim, "sq": rec["q_len"],
+                                          "capacity": rec["kv_len"], "lengths": lengths,
+                                          "lat": {}, "auto": {}})
+            # Explicit records measure even splits on the layout's default
+            # kernel; the automatic record's plan may differ (length-balanced
+            # splits, the single-stage kernel), so it stands for its split
+            # count only where no explicit record of that count exists.
+            lat = case["auto"] if rec.get("requested_splits") is None else case["lat"]
             s = rec["num_splits"]
-            case["lat"][s] = min(case["lat"].get(s, math.inf), rec["us_per_call"])
-            if rec.get("requested_splits") is None:
-                case["legacy"] = s  # the automatic choice when the scan was taken
+            lat[s] = min(lat.get(s, math.inf), rec["us_per_call"])
     if device is None:
         raise ValueError("scan records carry no device record")
+    for c in cases.values():
+        for s, t in c.pop("auto").items():
+            c["lat"].setdefault(s, t)
     return [c for c in cases.values() if len(c["lat"]) >= 2], _Device(*device)
 
 
@@ -129,8 +158,13 @@ def fit(cases, device, tolerance: float = 0.03, margin: float = 0.5) -> List[flo
 
 
 def evaluate(weights, cases, device, tolerance, margin) -> dict:
+    """Selection quality of the model over `cases` (chosen split's measured
+    latency / the case's best), and of the C fill rule over the cases whose
+    fill-rule split count was measured (fill_rule_unmeasured counts the
+    others; the model's figures on exactly those cases are model_on_fill_cases)."""
     model = {"weights": weights, "selection_tolerance": tolerance, "absolute_margin_us": margin}
-    ratios, legacy, rows = [], [], []
+    ratios, fill, model_on_fill, rows = [], [], [], []
+    unmeasured = 0
     for c in cases:
         preds = {s: M.predict(c["batch"], c["sq"], c["heads"], c["dim"], c["lengths"], s,
                               device.num_cus, device.wg_per_cu, model) for s in c["lat"]}
@@ -140,17 +174,35 @@ def evaluate(weights, cases, device, tolerance, margin) -> dict:
         best_s = min(c["lat"], key=c["lat"].get)
         r = c["lat"][chosen] / c["lat"][best_s]
         ratios.append(r)
-        if c["legacy"] is not None:
-            legacy.append(c["lat"][c["legacy"]] / c["lat"][best_s])
-        rows.append({"batch": c["batch"], "heads": c["heads"], "sq": c["sq"],
-                     "kv": c["capacity"], "chosen": chosen, "best": best_s,
+        fs = fill_rule_splits(c, device)
+        if fs in c["lat"]:
+            fill.append(c["lat"][fs] / c["lat"][best_s])
+            model_on_fill.append(r)
+        else:
+            unmeasured += 1
+        rows.append({"suite": c["suite"], "batch": c["batch"], "heads": c["heads"], "sq": c["sq"],
+                     "kv": c["capacity"], "chosen": chosen, "fill_rule": fs, "best": best_s,
                      "relative_to_best": round(r, 4)})
-    geo = lambda xs: math.exp(sum(map(math.log, xs)) / len(xs))  # noqa: E731
+    geo = lambda xs: math.exp(sum(map(math.log, xs)) / len(xs)) if xs else None  # noqa: E731
     return {"cases": len(ratios), "within_5pct": sum(r <= 1.05 for r in ratios),
             "geomean_relative_to_best": geo(ratios), "max_relative_to_best": max(ratios),
-            "legacy_cases": len(legacy),
-            "legacy_geomean_relative_to_best": geo(legacy) if legacy else None,
-            "legacy_max_relative_to_best": max(legacy) if legacy else None, "rows": rows}
+            "fill_rule_cases": len(fill), "fill_rule_unmeasured": unmeasured,
+            "fill_rule_geomean_relative_to_best": geo(fill),
+            "fill_rule_max_relative_to_best": max(fill) if fill else None,
+            "model_on_fill_cases_geomean": geo(model_on_fill),
+            "model_on_fill_cases_max": max(model_on_fill) if model_on_fill else None,
+            "fill_rule_within_5pct": sum(r <= 1.05 for r in fill), "rows": rows}
+
+
+def held_out(cases, device, suites, tolerance, margin) -> dict:
+    """Weights fitted on the cases outside `suites`, evaluated on those inside."""
+    train = [c for c in cases if c["suite"] not in suites]
+    test = [c for c in cases if c["suite"] in suites]
+    weights = fit(train, device, tolerance, margin)
+    rep = evaluate(weights, test, device, tolerance, margin)
+    return {"train_suites": sorted({c["suite"] for c in train}), "test_suites": sorted(suites),
+            "train_cases": len(train), "weights": weights,
+            **{k: v for k, v in rep.items() if k != "rows"}}
 
 
 def main(argv=None) -> int:
@@ -161,10 +213,13 @@ def main(argv=None) -> int:
     ap.add_argument("--tolerance", type=float, default=0.03,
                     help="relative score tolerance: the smallest split within it wins")
     ap.add_argument("--margin-us", type=float, default=0.5)
+    ap.add_argument("--holdout", nargs="*", default=list(HOLDOUT),
+                    help="suites left out of the held-out fit and evaluated on it")
     args = ap.parse_args(argv)
     cases, device = load_cases(args.scans)
     weights = fit(cases, device, args.tolerance, args.margin_us)
     report = evaluate(weights, cases, device, args.tolerance, args.margin_us)
+    holdout = held_out(cases, device, tuple(args.holdout), args.tolerance, args.margin_us)
     lens = [c["capacity"] for c in cases]
     sqs = [c["sq"] for c in cases]
     model = {
@@ -179,6 +234,7 @@ def main(argv=None) -> int:
                   "dims": sorted({c["dim"] for c in cases})},
         "training_cases": report["cases"],
         "in_sample": {k: v for k, v in report.items() if k != "rows"},
+        "held_out": holdout,
         "sources": [{"name": pathlib.Path(p).name,
                      "sha256": hashlib.sha256(pathlib.Path(p).read_bytes()).hexdigest()}
                     for p in args.scans],

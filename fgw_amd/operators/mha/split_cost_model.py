@@ -19,8 +19,11 @@ else 4 query-parallel waves over 128 rows, 64 keys per round):
   has_merge        s > 1
   partial_mbytes   s > 1: fp32 partial + LSE bytes written and read back, in MB
   merge_rows       s > 1: output rows merged x s / 1e3
-  longest_excess   key rounds of the longest request's split beyond the mean
-                   (ragged batches; general_split_cost_model.py:128-131)
+The reference's ragged-batch feature (the longest request's split rounds
+beyond the mean, general_split_cost_model.py:128-131) is not used: ragged
+batches run length-balanced splits here (balanced_split_keys), and on the
+calibration's ragged cases a fit that gives it weight chooses the same split
+counts as one without it.
 """
 from __future__ import annotations
 
@@ -32,8 +35,7 @@ from typing import Optional, Sequence
 
 MODEL_PATH = pathlib.Path(__file__).with_name("split_cost_model.json")
 SPLITS = (1, 2, 4, 8, 16, 32, 64, 128)
-FEATURE_NAMES = ("constant", "wave_rounds", "waves", "has_merge", "partial_mbytes", "merge_rows",
-                 "longest_excess")
+FEATURE_NAMES = ("constant", "wave_rounds", "waves", "has_merge", "partial_mbytes", "merge_rows")
 
 
 def geometry(sq: int, dim: int = 128):
@@ -58,7 +60,6 @@ def features(batch, sq, heads, dim, lengths: Sequence[int], splits, num_cus, wg_
     waves = math.ceil(items / slots)
     rounds = [math.ceil(n / keys_round) for n in lengths]
     longest = math.ceil(max(rounds) / splits) if rounds else 0
-    mean = (sum(rounds) / len(rounds)) / splits if rounds else 0.0
     multi = int(splits > 1)
     parts_mb = multi * batch * heads * splits * sq * (dim + 1) * 4 * 2 / 1e6
     # Critical path in key rounds per CU: the programs resident on one CU
@@ -66,7 +67,7 @@ def features(batch, sq, heads, dim, lengths: Sequence[int], splits, num_cus, wg_
     # ceil(items / CUs) items of `longest` rounds whatever its slot count.
     cu_rounds = math.ceil(items / num_cus) * longest
     return [1.0, cu_rounds * dim / 128.0, float(waves), float(multi), parts_mb,
-            multi * batch * heads * sq * splits / 1e3, max(0.0, longest - mean)]
+            multi * batch * heads * sq * splits / 1e3]
 
 
 @lru_cache(maxsize=2)
