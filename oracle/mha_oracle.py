@@ -11,6 +11,10 @@ Functions and the reference lines they follow:
   physical_rows        operators/mha/kernels/mha_paged_decode_ascend_v0.py:137
   reference            operators/mha/kernels/mha_paged_decode_ascend_v0.py:129-144
   chunked_reference    benchmarks/mha/bench_mha_mfu.py:38-60
+  rounded_reference    the reference kernel's rounding points: softmax in fp32 against the
+                       row maximum, row sum of the fp32 probabilities, P cast to the input
+                       dtype for PV (mha_paged_decode_ascend_v7.py:120-192, the vcvt at
+                       :159-162), O / l cast (:455-465)
   merge_partials       operators/mha/kernels/mha_paged_decode_ascend_v7.py:352-370
   partial_states       v7.py:305-315 (O/l, LSE = ln l + m; -1e30 when empty), over
                        the block partition of this build's kernel
@@ -32,7 +36,9 @@ Pinning (tests/test_oracle.py): the report vectors the reference recorded
 float64 brute-force softmax attention and closed forms (single key, equal
 keys, empty rows) pin reference/chunked_reference; the reference's raw
 partition-merge vectors (tests/mha/test_raw_partial_state.py) and a dense
-comparison pin merge_partials/partial_states; the published FLOP/byte counts
+comparison pin merge_partials/partial_states; its equality with reference for
+float32 inputs (where the cast is exact) and a two-key closed form of the
+rounded P pin rounded_reference; the published FLOP/byte counts
 pin useful_flops/algorithmic_bytes; exhaustive integer checks pin page_div;
 row-by-row resolution through physical_rows (live rows) and the original
 pages (page tails), plus closed forms of the offsets, pin packed_offsets and
@@ -100,6 +106,36 @@ def chunked_reference(q, k, v, table, lengths, page_size, causal, chunk=128):
             probabilities = scores.softmax(-1).nan_to_num(0.0)
             output[b, start:stop] = (probabilities @ vv).transpose(0, 1).to(q.dtype)
     return output
+
+
+def rounded_reference(q, k, v, table, lengths, page_size, causal):
+    """CPU attention with the rounding points of the reference kernel
+    (v7.py:120-192, :455-465): scores and the softmax against the row maximum
+    in fp32, the row sum of the fp32 probabilities, P cast to the input dtype
+    for the PV product (the vcvt at v7.py:159-162), PV in fp32, O / l cast to
+    the input dtype; rows with no visible key are zero. Its error against
+    `reference` is the error any kernel with these rounding points makes."""
+    q, k, v, table, lengths = [x.cpu() for x in (q, k, v, table, lengths)]
+    b, sq, h, d = q.shape
+    out = torch.zeros_like(q)
+    scale = d ** -0.5
+    for bi in range(b):
+        n = int(lengths[bi])
+        if n == 0:
+            continue
+        rows = physical_rows(table, bi, n, page_size)
+        kk, vv = k[rows].float(), v[rows].float()
+        vis = torch.tensor([visible_keys(n, sq, qi, causal) for qi in range(sq)])
+        for hi in range(h):
+            s_ = (q[bi, :, hi].float() @ kk[:, hi].T) * scale
+            s_ = s_.masked_fill(torch.arange(n)[None, :] >= vis[:, None], float("-inf"))
+            m = s_.max(dim=1, keepdim=True).values.clamp_min(-1e30)
+            p = torch.exp(s_ - m)
+            l_ = p.sum(dim=1, keepdim=True)
+            o = p.to(q.dtype).float() @ vv[:, hi]
+            res = torch.where(l_ > 0, o / l_.clamp_min(1e-30), torch.zeros_like(o))
+            out[bi, :, hi] = res.to(q.dtype)
+    return out
 
 
 def split_ranges(n_blocks: int, splits: int) -> List[Tuple[int, int]]:

@@ -5,7 +5,11 @@ reference code is imported or run) and writes accuracy_report_vectors.json:
 one entry per distinct (case, seed, pattern) with the shape, pool rows and the
 per-request cache lengths the reference's harness generated
 (tests/mha/test_mha_paged_accuracy.py:73-101, :219-222). These pin the
-oracle's lengths_for / make_inputs restatements.
+oracle's lengths_for / make_inputs restatements. It also writes
+accuracy_report_ratios.json: every recorded check (case, seed, dtype, causal,
+pattern) with the reference kernel's max error / tolerance ratio at the
+harness tolerances (test_mha_paged_accuracy.py:259-273), the figures this
+build's accuracy is compared with check by check.
 
 Run once in the build container: python tests/golden/make_report_vectors.py
 """
@@ -22,14 +26,22 @@ SOURCES = (
     "mha_persistent28_causal.json",
 )
 OUT = pathlib.Path(__file__).with_name("accuracy_report_vectors.json")
+RATIOS = pathlib.Path(__file__).with_name("accuracy_report_ratios.json")
 
 
 def main() -> int:
-    seen, vectors = set(), []
+    seen, vectors, ratios = set(), [], []
     for name in SOURCES:
         report = json.loads((REPORTS / name).read_text(encoding="utf-8"))
         for entry in report["results"]:
             shape = entry["shape"]
+            if entry.get("status") == "passed" and "max_tolerance_ratio" in entry:
+                ratios.append({
+                    "source": name, "case": entry["case"], "seed": entry["seed"],
+                    "dtype": entry["dtype"].replace("torch.", ""), "causal": entry["causal"],
+                    "pattern": entry["pattern"], "rtol": entry["rtol"], "atol": entry["atol"],
+                    "max_tolerance_ratio": entry["max_tolerance_ratio"],
+                })
             key = (entry["case"], entry["seed"], entry["pattern"])
             if key in seen:
                 continue
@@ -44,6 +56,11 @@ def main() -> int:
     OUT.write_text(json.dumps({"note": "extracted from the reference's recorded accuracy reports",
                                "vectors": vectors}, indent=1) + "\n", encoding="utf-8")
     print(f"wrote {len(vectors)} vectors to {OUT}")
+    lines = ",\n".join(json.dumps(r, separators=(",", ":")) for r in ratios)
+    RATIOS.write_text('{"note": "per-check max error / tolerance of the reference kernel, from '
+                      'its recorded accuracy reports",\n"checks": [\n' + lines + "\n]}\n",
+                      encoding="utf-8")
+    print(f"wrote {len(ratios)} checks to {RATIOS}")
     return 0
 
 

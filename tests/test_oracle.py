@@ -296,3 +296,54 @@ def test_imbalanced_lengths_recipe():
         assert got.dtype == torch.int32 and got.tolist() == want
         assert all(kv // 8 <= n <= kv for n in want)
     assert O.imbalanced_lengths(8192, seed=8).tolist() != expected[8192]
+
+
+def test_rounded_reference_pins():
+    """rounded_reference (the reference kernel's rounding points): with
+    float32 inputs the cast of P is exact and it equals reference; a two-key
+    row follows the closed form (v0 + p v1) / (1 + p) with p cast to bfloat16
+    in the numerator only."""
+    case = ("pin", 2, 3, 2, 32, 16, 3)
+    q, k, v, table = O.make_inputs(case, 11, torch.float32)
+    lengths = torch.tensor([37, 5], dtype=torch.int32)
+    for causal in (False, True):
+        torch.testing.assert_close(O.rounded_reference(q, k, v, table, lengths, 16, causal),
+                                   O.reference(q, k, v, table, lengths, 16, causal),
+                                   rtol=1e-5, atol=1e-6)
+    d = 16
+    q1 = torch.zeros(1, 1, 1, d, dtype=torch.bfloat16)
+    q1[0, 0, 0, 0] = 1.0
+    k1 = torch.zeros(2, 1, d, dtype=torch.bfloat16)
+    k1[1, 0, 0] = -3.0  # score difference 3 / sqrt(16) = 0.75
+    v1 = torch.zeros(2, 1, d, dtype=torch.bfloat16)
+    v1[0, 0, 0], v1[1, 0, 0] = 1.0, 8.0
+    table1 = torch.tensor([[0]], dtype=torch.int32)
+    got = O.rounded_reference(q1, k1, v1, table1, torch.tensor([2], dtype=torch.int32), 2, False)
+    p = math.exp(-0.75)
+    p16 = float(torch.tensor(p).to(torch.bfloat16))
+    assert p16 != p
+    want = float(torch.tensor((1.0 + 8.0 * p16) / (1.0 + p)).to(torch.bfloat16))
+    assert float(got[0, 0, 0, 0]) == want
+
+
+@pytest.mark.parametrize("name,seed,causal,pattern,ratio", [
+    ("cube_direct_q129", 42, True, "mixed", 0.733),
+    ("cube_direct_q1024", 7, True, "mixed", 0.710),
+    ("cube_q257", 2026, True, "full", 0.676),
+    ("dim128", 2026, False, "mixed", 0.639),
+])
+def test_rounding_points_set_the_worst_accuracy_checks(name, seed, causal, pattern, ratio):
+    """The accuracy suite's worst BF16 checks: the reference kernel's rounding
+    points alone (rounded_reference) reach these error / tolerance ratios
+    against the fp32 reference; the HIP kernel's ratios on the same checks are
+    the same (tests/test_accuracy_vs_reference.py). dim128 is the reference's
+    own recorded worst check (0.639, mha_cube_general_accuracy.json); the
+    causal CUBE checks are outside its reports."""
+    case = mha_cases.ALL_CASES[name]
+    q, k, v, table = O.make_inputs(case, seed, torch.bfloat16)
+    lengths = torch.tensor(O.lengths_for(case, pattern, seed), dtype=torch.int32)
+    exp = O.chunked_reference(q, k, v, table, lengths, case[5], causal, 128)
+    got = O.rounded_reference(q, k, v, table, lengths, case[5], causal)
+    rtol, atol = O.TOLERANCES[torch.bfloat16]
+    r = ((got.float() - exp.float()).abs() / (atol + rtol * exp.float().abs())).max().item()
+    assert r == pytest.approx(ratio, abs=0.001)
