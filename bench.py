@@ -59,13 +59,15 @@ def parse():
                     help="only run a plain 1 GiB device copy (counter calibration) and exit")
     ap.add_argument("--suite", default="headline",
                     choices=("headline", "decode-scan", "decode-batch", "grid", "prefill",
-                             "static", "power", "scans"),
+                             "static", "static-scan", "power", "scans"),
                     help="headline: the one-line bench contract (default). decode-scan: "
                          "config 4 split scan; decode-batch: Q1 decode split scan over larger "
                          "batches and head counts (split cost model calibration); grid: "
                          "config 2 short-Q grid; "
                          "prefill: Q4096 and Q32768; static: B1H1 static-plan path against "
-                         "the automatic split path; power: MFMA rate on N(0,1) against "
+                         "the automatic split path; static-scan: the same over a Q x KV grid "
+                         "(calibration of the static builders' fallback); power: MFMA rate "
+                         "on N(0,1) against "
                          "constant inputs (library GEMM and the headline kernel); scans: the "
                          "first four scan suites")
     ap.add_argument("--out", default=None, help="scan suites: JSONL file for the records "
@@ -392,34 +394,52 @@ STATIC_SHAPES = ((128, 512), (512, 2048), (1024, 4096), (3712, 4096), (4096, 204
                  (16384, 1024), (64, 32768), (5000, 2048), (2048, 16384))
 
 
-def suite_static(args, emit):
+STATIC_SCAN_Q = (64, 128, 256, 512, 1024, 2048, 3712, 4096, 5000, 8192, 16384)
+STATIC_SCAN_KV = (512, 1024, 2048, 4096, 8192, 16384, 32768)
+
+
+def suite_static(args, emit, shapes=None, suite="static"):
     """B1H1 D128 BF16 full page-128 KV: the static-plan path (choose_stream_plan,
-    the reference's fused B1H1 entry) against the automatic split path, GPU
-    time per call from graph replays; both checked against the oracle."""
+    the reference's fused B1H1 entry, its own plan whatever the fallback would
+    choose) against the automatic split path, GPU time per call from graph
+    replays; both checked against the oracle (sampled rows from Q 4096)."""
     import torch
     from fgw_amd.operators.mha import static_schedule as S
     from fgw_amd.operators.mha.current import build_kernel
     from fgw_amd.operators.mha.kernels.mha_static_host_hip import build_fused_kernel
     from oracle import mha_oracle as O
     dev = torch.device("cuda", 0)
-    for sq, kv in STATIC_SHAPES:
+    for sq, kv in shapes or STATIC_SHAPES:
         host = O.bench_inputs(1, sq, 1, 128, 128, kv, torch.bfloat16)
         dinputs = [x.to(dev) for x in host]
-        expected = O.chunked_reference(*host, 128, False, 128)
+        rows = list(range(sq)) if sq <= 4096 else list(range(256)) + list(range(sq - 256, sq))
+        expected = O.chunked_reference(host[0][:, rows], *host[1:], 128, False, 128)
         auto = build_kernel(1, sq, 1, 128, host[1].shape[0], kv // 128, 128, False, "bfloat16", 0,
                             full_kv_cache=True)
-        static = build_fused_kernel(sq, kv, host[1].shape[0], 0)
-        _checked(auto, dinputs, expected, torch.bfloat16, f"static-suite auto q{sq} kv{kv}")
-        _checked(static, dinputs, expected, torch.bfloat16, f"static-suite static q{sq} kv{kv}")
+        static = build_fused_kernel(sq, kv, host[1].shape[0], 0, fallback=False)
+        for kern, name in ((auto, "auto"), (static, "static")):
+            got = kern(*dinputs)
+            torch.cuda.synchronize()
+            rtol, atol = O.TOLERANCES[torch.bfloat16]
+            torch.testing.assert_close(got[:, rows].cpu(), expected, rtol=rtol, atol=atol,
+                                       msg=lambda m: f"{suite} {name} q{sq} kv{kv}: {m}")
         t_auto = graph_us(lambda: auto(*dinputs))
         t_static = graph_us(lambda: static(*dinputs))
         d = static.plan.describe()
-        emit({"suite": "static", "q_len": sq, "kv_len": kv, "auto_us": t_auto,
-              "auto_splits": auto.num_splits, "auto_layout": auto.layout, "static_us": t_static,
+        emit({"suite": suite, "q_len": sq, "kv_len": kv, "auto_us": t_auto,
+              "auto_splits": auto.num_splits, "auto_layout": auto.layout,
+              "auto_grid": auto.compute_grid, "auto_work": auto.compute_work,
+              "static_us": t_static,
               "static_strategy": d["strategy"], "static_programs": d["programs"],
               "static_merged_tiles": d["merge_q_tiles"],
               "static_estimate_us": S.estimate_cost(static.plan)["total_us"],
               "speedup": t_auto / t_static})
+
+
+def suite_static_scan(args, emit):
+    """suite_static over STATIC_SCAN_Q x STATIC_SCAN_KV."""
+    suite_static(args, emit, [(q, kv) for q in STATIC_SCAN_Q for kv in STATIC_SCAN_KV],
+                 "static-scan")
 
 
 def suite_power(args, emit):
@@ -466,7 +486,8 @@ def run_scans(args):
     torch.cuda.set_device(0)
     suites = {"decode-scan": [suite_decode_scan], "decode-batch": [suite_decode_batch],
               "grid": [suite_grid],
-              "prefill": [suite_prefill], "static": [suite_static], "power": [suite_power],
+              "prefill": [suite_prefill], "static": [suite_static],
+              "static-scan": [suite_static_scan], "power": [suite_power],
               "scans": [suite_prefill, suite_decode_scan, suite_grid, suite_static]}[args.suite]
     out = open(args.out, "w") if args.out else None
     records = []

@@ -41,6 +41,8 @@ def _device_programs(device_index):
 class _StaticLaunch:
     """Launch callable of one (plan, Q, KV, pool) specialisation."""
 
+    execution = "static"
+
     def __init__(self, plan, sq, kv, pool_rows, device_index, meta):
         self.plan = plan
         self._sq, self._kv, self._pool = sq, kv, pool_rows
@@ -203,14 +205,69 @@ def build_kernel(sq, kv, pool_rows, plan_policy="balanced", programs=None, merge
     return launch
 
 
+class _AutomaticLaunch:
+    """The static builder's fallback: the same call signature and two-phase
+    entry points (compute, then finish) over the automatic split path
+    (build_kernel of the main entry), for shapes where that path measured
+    faster. `plan` is the static plan it replaced (for describe()); `execution`
+    says which path runs."""
+
+    execution = "automatic"
+
+    def __init__(self, plan, sq, kv, pool_rows, device_index):
+        from fgw_amd.operators.mha.kernels.mha_paged_decode_hip import build_kernel as _build
+        self.plan = plan
+        self._sq, self._kv, self._pool, self._width = sq, kv, pool_rows, kv // PAGE
+        self._kernel = _build(1, sq, 1, D, pool_rows, self._width, PAGE, False, "bfloat16",
+                              device_index, full_kv_cache=True)
+        self.compute_grid = self._kernel.compute_grid
+        self.num_splits = self._kernel.num_splits
+        self.layout = self._kernel.layout
+        self.plan_policy = "automatic"
+        self.merge_policy = "rawsimd"
+        self.local_kernel = self.compute
+        self.merge_kernel = None
+        self.fixed_merge_kernel = None
+        self.merge_assignment = dict(policy="automatic", tasks=(), programs=0, max_rows=S.BLOCK,
+                                     max_chunks=1)
+
+    def validate_inputs(self, q, k, v, table, lengths):
+        """The reference's input assertions (mha_static_host_candidate.py:502-509)."""
+        assert tuple(q.shape) == (1, self._sq, 1, D) and tuple(k.shape) == (self._pool, 1, D)
+        assert v.shape == k.shape
+        assert tuple(table.shape) == (1, self._width) and lengths.cpu().tolist() == [self._kv]
+        assert q.dtype == k.dtype == v.dtype == torch.bfloat16
+        assert table.dtype == lengths.dtype == torch.int32
+
+    def compute(self, q, k, v, table, lengths):
+        return None, None, self._kernel(q, k, v, table, lengths)
+
+    def run_local(self, prepared, k, v, table, lengths):
+        return self.compute(prepared, k, v, table, lengths)
+
+    def finish(self, parts, lse, output):
+        return output.view(1, self._sq, 1, D)
+
+    def __call__(self, q, k, v, table, lengths):
+        return self.finish(*self.compute(q, k, v, table, lengths))
+
+
 @lru_cache(maxsize=64)
-def build_fused_kernel(sq, kv, pool_rows, device_index=None):
+def build_fused_kernel(sq, kv, pool_rows, device_index=None, fallback=True):
     """Fused-output static path (mha_paged_decode_ascend_fused.py:357-680):
-    choose_stream_plan over the device's programs."""
+    choose_stream_plan over the device's programs.
+
+    fallback (default): where the automatic split path of the main entry
+    measured faster (static_schedule.static_preferred: the nearest shape of the
+    committed MI355X static-scan calibration, static kept from 1.02x), the
+    returned callable runs that path instead (`execution` == "automatic");
+    fallback=False always runs the static plan (`execution` == "static")."""
     if device_index is None:
         device_index = torch.cuda.current_device()
     plan = S.choose_stream_plan(sq, kv, _device_programs(int(device_index)))
     _check_pool(kv, pool_rows)
+    if fallback and not S.static_preferred(sq, kv):
+        return _AutomaticLaunch(plan, sq, kv, pool_rows, int(device_index))
     launch = _StaticLaunch(plan, sq, kv, pool_rows, int(device_index),
                            dict(plan_policy="stream", merge_policy="rawsimd"))
     launch.fixed_merge_kernel = None

@@ -22,6 +22,9 @@ terms of this build's kernels (below), fitted on MI355X, not the Ascend ones.
 """
 from __future__ import annotations
 
+import json
+import math
+import pathlib
 from dataclasses import dataclass
 from functools import lru_cache
 
@@ -308,3 +311,40 @@ def choose_stream_plan(q, kv, cores=DEFAULT_CORES):
     if estimate_cost(direct)["total_us"] - estimate_cost(split)["total_us"] > COST_MODEL["block_us"]:
         return split
     return direct
+
+
+# Fallback of the static builder (build_fused_kernel): the automatic split path
+# is faster at most B1H1 shapes on MI355X, and the two estimates (estimate_cost
+# above and any comparable model of the automatic plans) miss by 10% on median,
+# more than the paths usually differ, so the choice is read from measurements:
+# `python bench.py --suite static-scan` timed both paths (GPU time per call
+# from graph replays, checked against the oracle) over Q 64..16384 x KV
+# 512..32768 (calibration/mi355x_static_scan.jsonl); the static plan is kept
+# where the nearest measured shape (in log2 Q, log2 KV) ran it at least
+# STATIC_MIN_SPEEDUP times as fast as the automatic path.
+STATIC_CALIBRATION = pathlib.Path(__file__).with_name("calibration") / "mi355x_static_scan.jsonl"
+STATIC_MIN_SPEEDUP = 1.02
+
+
+@lru_cache(maxsize=1)
+def static_calibration() -> tuple:
+    """((Q, KV, automatic us, static us), ...) of the committed static-scan records."""
+    out = []
+    for line in STATIC_CALIBRATION.read_text().splitlines():
+        rec = json.loads(line)
+        if rec.get("suite") == "static-scan":
+            out.append((rec["q_len"], rec["kv_len"], rec["auto_us"], rec["static_us"]))
+    if not out:
+        raise ValueError(f"{STATIC_CALIBRATION} holds no static-scan records")
+    return tuple(out)
+
+
+def static_preferred(q: int, kv: int) -> bool:
+    """True where the static plan measured at least STATIC_MIN_SPEEDUP times
+    as fast as the automatic split at the nearest calibrated shape."""
+    _check_args(q, kv, 1)
+    lq, lk = math.log2(q), math.log2(kv)
+    nq, nk, auto_us, static_us = min(
+        static_calibration(), key=lambda r: ((math.log2(r[0]) - lq) ** 2 + (math.log2(r[1]) - lk) ** 2,
+                                             r[0], r[1]))
+    return auto_us >= STATIC_MIN_SPEEDUP * static_us

@@ -79,7 +79,8 @@ def test_graph_replays_of_the_static_fused_path():
     sq, kv = 512, 2048
     host = O.bench_inputs(1, sq, 1, 128, 128, kv, torch.bfloat16)
     dq, dk, dv, dt, dl = (x.cuda() for x in host)
-    kern = build_fused_kernel(sq, kv, host[1].shape[0], 0)
+    kern = build_fused_kernel(sq, kv, host[1].shape[0], 0, fallback=False)
+    assert kern.execution == "static"
     print(f"graph replay static fused: Q{sq} KV{kv} {kern.plan.describe()}", flush=True)
     assert kern.plan.merges  # cut tiles: the merge launch is captured too
     call = lambda: kern(dq, dk, dv, dt, dl)  # noqa: E731

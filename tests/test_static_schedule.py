@@ -198,16 +198,42 @@ def test_static_path_matches_oracle(sq, kv, policy, programs):
 def test_fused_static_path_matches_oracle():
     from fgw_amd.operators.mha.kernels.mha_static_host_hip import build_fused_kernel
     from oracle import mha_oracle as O
-    for sq, kv in ((64, 4096), (3712, 2048), (16384, 1024)):
+    from fgw_amd.operators.mha.current import build_kernel
+    for sq, kv in ((64, 4096), (3712, 2048), (16384, 1024), (1024, 1024)):
         q, k, v, table, lengths = _static_inputs(sq, kv, 7 + sq)
-        launch = build_fused_kernel(sq, kv, k.shape[0], 0)
-        print(f"fused static sq={sq} kv={kv}: {launch.plan.describe()}", flush=True)
-        got = launch(*[x.cuda() for x in (q, k, v, table, lengths)])
-        torch.cuda.synchronize()
+        dev = [x.cuda() for x in (q, k, v, table, lengths)]
         expected = (O.chunked_reference if sq > 256 else O.reference)(
             q, k, v, table, lengths, 128, False)
         rtol, atol = O.TOLERANCES[torch.bfloat16]
-        torch.testing.assert_close(got.cpu(), expected, rtol=rtol, atol=atol)
+        for fallback in (False, True):
+            launch = build_fused_kernel(sq, kv, k.shape[0], 0, fallback=fallback)
+            want = "static" if not fallback or S.static_preferred(sq, kv) else "automatic"
+            assert launch.execution == want, (sq, kv, fallback)
+            print(f"fused static sq={sq} kv={kv} fallback={fallback}: {launch.execution} "
+                  f"{launch.plan.describe()}", flush=True)
+            got = launch(*dev)
+            parts, lse, out = launch.compute(*dev)
+            again = launch.finish(parts, lse, out)
+            torch.cuda.synchronize()
+            torch.testing.assert_close(got.cpu(), expected, rtol=rtol, atol=atol)
+            assert torch.equal(again, got)
+            if launch.execution == "automatic":  # the main entry's own call, same bits
+                auto = build_kernel(1, sq, 1, 128, k.shape[0], kv // 128, 128, False, "bfloat16",
+                                    0, full_kv_cache=True)
+                assert torch.equal(got, auto(*dev))
+
+
+def test_static_fallback_follows_the_calibration():
+    """build_fused_kernel keeps the static plan exactly where the committed
+    MI355X static scan measured it >= 1.02x as fast as the automatic split
+    (at calibrated shapes; elsewhere the nearest one decides)."""
+    records = S.static_calibration()
+    assert len(records) >= 70
+    for q, kv, auto_us, static_us in records:
+        assert S.static_preferred(q, kv) == (auto_us >= S.STATIC_MIN_SPEEDUP * static_us), (q, kv)
+    assert S.static_preferred(1024, 1024) and S.static_preferred(16384, 1024)
+    assert not S.static_preferred(4096, 2048) and not S.static_preferred(64, 32768)
+    assert S.static_preferred(1152, 1152) == S.static_preferred(1024, 1024)  # nearest shape
 
 
 @pytest.mark.gpu
