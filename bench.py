@@ -26,6 +26,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import os
 import pathlib
 import re
 import statistics
@@ -51,7 +52,9 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--cpu-threads", type=int, default=0, help="0 = torch's default thread count")
+    ap.add_argument("--cpu-threads", type=int, default=0,
+                    help="CPU baseline's full thread count; 0 = every CPU of the process's "
+                         "affinity set")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="wall-clock bound of the CPU baseline sample at full thread count")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -644,7 +647,10 @@ def prefill_record(kern, inputs, flops, qkv_bytes, steps, warmup, samples):
         "roofline": {"bound": "mfma", "kernel": PREFILL_KERNELS[kern.layout],
                      "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / PEAK_BF16_TFLOPS, "kernel_us": kernel_ms * 1e3,
-                     "kernel_us_source": "back-to-back region / calls (HIP events, launch stream)",
+                     "kernel_us_source": "average launch duration: one event pair around the "
+                                         "back-to-back region of the calls (one kernel each) on "
+                                         "the launch stream / calls; includes the dispatch gap "
+                                         "between launches",
                      "algorithmic_flops": flops, "algorithmic_bytes": qkv_bytes},
     }
 
@@ -691,7 +697,11 @@ def main():
     from oracle import mha_oracle as O
 
     dev = torch.device("cuda", 0)
-    cores = args.cpu_threads or torch.get_num_threads()
+    # The CPU baseline's full leg runs on every CPU this process may use (its
+    # affinity set: on the GPU boxes a share of the host, whatever
+    # os.cpu_count() reports for the whole machine); both counts are recorded.
+    affinity = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else None
+    cores = args.cpu_threads or affinity or os.cpu_count() or torch.get_num_threads()
     rtol, atol = O.TOLERANCES[torch.bfloat16]
     b, h, d, page, kv = 2, 8, 128, 128, 2048
 
@@ -784,12 +794,15 @@ def main():
         base, expected = cpu_baselines(host, dsmall, page, flops, cores, args.cpu_seconds)
         full = base["prefill"][str(cores)]
         cpu = {"value": full["tflops"], "unit": "TFLOP/s", "cores": cores, "kind": "port",
-               "cpu_model": base["cpu_model"],
+               "cpu_model": base["cpu_model"], "os_cpu_count": os.cpu_count(),
+               "affinity_cpus": affinity,
+               "omp_num_threads": os.environ.get("OMP_NUM_THREADS"),
                "sample": f"whole Q4096/KV2048 B2H8 D128 workload, oracle chunked_reference "
                          f"(torch fp32, chunk 128), median of {full['runs']} runs at "
-                         f"torch.set_num_threads({cores}); value_4_threads at 4 threads (the "
-                         "reference harness cap); decode: Q1 at KV 512/2048/8192/32768 and "
-                         "config 1, each at 4 and full threads",
+                         f"torch.set_num_threads({cores}) (every CPU of the process's affinity "
+                         f"set: {affinity}; os.cpu_count() {os.cpu_count()}); value_4_threads "
+                         "at 4 threads (the reference harness cap); decode: Q1 at KV "
+                         "512/2048/8192/32768 and config 1, each at 4 and full threads",
                "seconds_per_call": full["seconds_per_call"],
                "value_4_threads": base["prefill"]["4"]["tflops"],
                "decode": base["decode"]}
