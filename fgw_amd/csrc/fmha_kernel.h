@@ -584,8 +584,10 @@ __device__ __forceinline__ void store_row(const FwdParams& p, int b, int h, int 
 // chunk c of staged row r sits at chunk c ^ (r % chunks per row), so both
 // the column writes of 32 rows and the row reads spread over all banks.
 // bf16/fp16 rows (f32 false) go to bdst + r * brow_stride bytes, all DPAD
-// dims in one pass; fp32 rows (f32 true) to fdst + r * DPAD floats, 64 dims
-// (256 bytes per row) per pass. Rows r >= rows are not stored.
+// dims in one pass, with non-temporal stores (the final output: nothing in
+// the kernel reads it again); fp32 rows (f32 true, split partials that the
+// merge reads back) to fdst + r * DPAD floats, 64 dims (256 bytes per row)
+// per pass. Rows r >= rows are not stored.
 template <class C>
 constexpr int kStagedRowBytes = 2 * C::DPAD > 256 ? 2 * C::DPAD : 256;
 
@@ -640,7 +642,8 @@ __device__ __forceinline__ void store_rows_staged(unsigned char* st, int lane,
     for (int k = 0; k < 32 / RPI; ++k) {
       const int r = RPI * k + lane / NCH, c = lane % NCH;
       const u32x4 v = *reinterpret_cast<const u32x4*>(st + r * RB + 16 * (c ^ (r % NCH)));
-      if (r < rows) *reinterpret_cast<u32x4*>(bdst + r * brow_stride + 16 * c) = v;
+      if (r < rows)
+        __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(bdst + r * brow_stride + 16 * c));
     }
   }
 }

@@ -48,10 +48,14 @@
 // correct because loads retire in order.
 //
 // Operand addresses. Each lane keeps the LDS address of its K operand for
-// every k-step (the K chunks are XOR-swizzled per row, so the eight differ
-// per lane) and the base of its V^T reads; a matrix phase adds the ring
-// slot once per k-step, and every other part of an address (S^T tile, PV
-// k-step) is an immediate offset of the LDS read.
+// every k-step and of its V^T reads for every O^T tile (the chunks are
+// XOR-swizzled per row, so they differ per lane); the main loops are unrolled
+// over the four ring slots, so every other part of an address (slot, S^T
+// tile, PV k-step) is an immediate offset of the LDS read.
+//
+// Q is loaded and O stored with non-temporal hints: each is touched once,
+// while the K/V blocks of (b, h) are read again by its other query tiles
+// from the L2.
 #pragma once
 #include <utility>
 
@@ -203,29 +207,30 @@ struct BlockDma {
 template <class C>
 __device__ __forceinline__ void issue_fast_block(const char* kbase, const char* vbase, u32 kdst,
                                                  u32 vdst, const BlockDma<C>& bd, int wave) {
+  // Instruction q of the wave fills 1 KB number q NWQ + wave of each tile.
+  const u32 kw = kdst + 1024u * (u32)wave, vw = vdst + 1024u * (u32)wave;
 #pragma unroll
   for (int q = 0; q < C::INSTR_PER_WAVE; ++q) {
-    const u32 ii = (u32)(q * C::NWQ + wave);
-    dma_saddr(kbase, bd.k[q], kdst + 1024u * ii);
-    dma_saddr(vbase, bd.v[q], vdst + 1024u * ii);
+    dma_saddr(kbase, bd.k[q], kw + 1024u * (u32)(q * C::NWQ));
+    dma_saddr(vbase, bd.v[q], vw + 1024u * (u32)(q * C::NWQ));
   }
 }
 
 // Per-lane LDS byte addresses of the MFMA A operands, ring bases included:
 //   K (k-step kk):  kring + k_base + 32 (kk ^ ky)          (+ slot, + 32 t rows)
 //   V (O^T tile dt): vring + v_base + 64 (dt ^ vy)         (+ slot, + 16 k2 rows)
-// The slot and row parts are compile-time constants of the matrix phase, so
-// every operand read is one of these registers plus an immediate offset.
+// The row parts are compile-time constants of the matrix phase and so is the
+// slot in the unrolled main loops, so there every operand read is one of
+// these registers plus an immediate offset.
 template <class C>
 struct OperandAddr {
   u32 k[C::KK];
-  u32 v;  // vring + v_base
-  int vy;
+  u32 v[C::DT];
   __device__ __forceinline__ OperandAddr(const Lanes<C>& ln, u32 kring, u32 vring) {
 #pragma unroll
     for (int kk = 0; kk < C::KK; ++kk) k[kk] = kring + (u32)(ln.k_base + 32 * (kk ^ ln.ky));
-    v = vring + (u32)ln.v_base;
-    vy = ln.vy;
+#pragma unroll
+    for (int dt = 0; dt < C::DT; ++dt) v[dt] = vring + (u32)(ln.v_base + 64 * (dt ^ ln.vy));
   }
 };
 
@@ -252,7 +257,7 @@ __device__ __forceinline__ void matrix_phase(const OperandAddr<C>& ad, u32 koff,
     constexpr int i = decltype(ic)::value;
     if constexpr (i < NPV) {
       constexpr int dt = i % C::DT, k2 = i / C::DT;
-      lds_byte* va = lds_at(ad.v + 64 * (dt ^ ad.vy) + voff) + 16 * k2 * C::ROW_BYTES;
+      lds_byte* va = lds_at(ad.v[dt]) + voff + 16 * k2 * C::ROW_BYTES;
       const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)va);
       const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
           (__attribute__((address_space(3))) i16x4*)(va + 8 * C::ROW_BYTES));
@@ -260,7 +265,7 @@ __device__ __forceinline__ void matrix_phase(const OperandAddr<C>& ad, u32 koff,
       return u32x4{lo2.x, lo2.y, hi2.x, hi2.y};
     } else {
       constexpr int t = (i - NPV) % C::ST, kk = (i - NPV) / C::ST;
-      return *(const __attribute__((address_space(3))) u32x4*)(lds_at(ad.k[kk] + koff) +
+      return *(const __attribute__((address_space(3))) u32x4*)(lds_at(ad.k[kk]) + koff +
                                                                t * 32 * C::ROW_BYTES);
     }
   };
@@ -293,14 +298,28 @@ __device__ __forceinline__ void matrix_phase(const OperandAddr<C>& ad, u32 koff,
   __builtin_amdgcn_s_setprio(0);
 }
 
+// Scores of keys at or beyond the lane's visible count become -inf: element
+// (t, v) holds key pos0 + 4 (lane / 32) + 32 t + 8 (v / 4) + v % 4, masked
+// when 32 t + 8 (v / 4) + v % 4 >= lim = vis - 4 (lane / 32) - pos0.
+template <class C>
+__device__ __forceinline__ void mask_from(f32x16 (&s)[C::ST], int lim) {
+#pragma unroll
+  for (int t = 0; t < C::ST; ++t)
+#pragma unroll
+    for (int v = 0; v < 16; ++v)
+      if (32 * t + 8 * (v >> 2) + (v & 3) >= lim) s[t][v] = -INFINITY;
+}
+
 template <class C>
 __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p,
                                                              const int32_t* __restrict__ table,
                                                              const int32_t* __restrict__ lengths) {
   __shared__ __attribute__((aligned(1024))) unsigned char smem[C::LDS_BYTES];
   unsigned char* const kring = smem;
-  unsigned char* const vring = smem + C::NKSLOT * C::TILE_BYTES;
-  const u32 kring_lds = lds_address(kring), vring_lds = lds_address(vring);
+  // The V ring's address from the K ring's (a generic pointer would be
+  // null-checked at every use).
+  const u32 kring_lds = lds_address(kring);
+  const u32 vring_lds = kring_lds + (u32)(C::NKSLOT * C::TILE_BYTES);
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -379,7 +398,9 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p,
     // Issued before len is known, so that the round trips overlap: the page
     // ids of the first 64-block window for a full cache (read again below if
     // len moves the item's first key; split 0 always starts at key 0), then
-    // Q^T (B of the QK^T product).
+    // Q^T (B of the QK^T product). Q is read once: non-temporal loads, which
+    // leave the L2 to the K/V blocks that the other query tiles of (b, h)
+    // read again.
     const int key0_full = first_block(capacity) * C::BN;
     int32_t id_first = block_page_id<C>(p, table_b, key0_full, lane);
     u32x4 qf[C::KK];
@@ -390,7 +411,8 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p,
       for (int kk = 0; kk < C::KK; ++kk) {
         const int d = 16 * kk + 8 * hh;
         u32x4 val = {0u, 0u, 0u, 0u};
-        if (qrow < p.sq && d < p.dim) val = load16(qp + d);
+        if (qrow < p.sq && d < p.dim)
+          val = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(qp + d));
         qf[kk] = val;
       }
     }
@@ -478,23 +500,24 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p,
       else
         win0.off = block_offset<C>(p, table_b, row_bytes, key0, N, len, lane);
       BlockWindow win1{1, 0};
-      // K and V of block j < N into K slot j % 4, V slot j % 4.
-      auto issue_block = [&](int j) {
+      // K and V of block j < N into K slot j % 4, V slot j % 4 (jslot: an
+      // int, or a compile-time constant in the unrolled loops).
+      auto issue_block = [&](int j, auto jslot) {
         if ((j >> 6) != win0.w) {  // uniform: the block entered the next window
           win0 = win1;
           win1 = BlockWindow{win0.w + 1, block_offset<C>(p, table_b, row_bytes, key0, N, len,
                                                          64 * (win0.w + 1) + lane)};
         }
         const int64_t off = readlane64(win0.off, j & 63);
-        const u32 kdst = kring_lds + (u32)((j % C::NKSLOT) * C::TILE_BYTES);
-        const u32 vdst = vring_lds + (u32)((j % C::NVSLOT) * C::TILE_BYTES);
-        if (off >= 0) {
+        const u32 kdst = kring_lds + (u32)((int)jslot * C::TILE_BYTES);
+        const u32 vdst = vring_lds + (u32)((int)jslot * C::TILE_BYTES);
+        if ((int32_t)((uint64_t)off >> 32) >= 0) {  // off >= 0 as a scalar compare
           issue_fast_block<C>(kb + off, vb + off, kdst, vdst, bd, wave);
         } else {
-          issue_slow_tile<C, false>(p, table_b, kb, row_bytes, key0 + j * C::BN, len, kdst, wave,
-                                    lane);
-          issue_slow_tile<C, true>(p, table_b, vb, row_bytes, key0 + j * C::BN, len, vdst, wave,
-                                   lane);
+          int pos0 = key0 + j * C::BN;
+          asm volatile("" : "+s"(pos0));  // no per-block induction variables for the rare path
+          issue_slow_tile<C, false>(p, table_b, kb, row_bytes, pos0, len, kdst, wave, lane);
+          issue_slow_tile<C, true>(p, table_b, vb, row_bytes, pos0, len, vdst, wave, lane);
         }
       };
       // Wait until block j has landed, the batch of block j + 1 (issued
@@ -505,8 +528,12 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p,
         else
           wait_vm<0>();
       };
-      issue_block(0);
-      if (1 < N) issue_block(1);
+      constexpr std::integral_constant<int, 0> s0{};
+      constexpr std::integral_constant<int, 1> s1{};
+      constexpr std::integral_constant<int, 2> s2{};
+      constexpr std::integral_constant<int, 3> s3{};
+      issue_block(0, s0);
+      if (1 < N) issue_block(1, s1);
 
       win1.off = block_offset<C>(p, table_b, row_bytes, key0, N, len, 64 + lane);
       wait_block(0);
@@ -522,19 +549,23 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p,
       u32x4 pf[C::KS];
 
       // M(n): PV of block n - 1 (V slot (n + 3) % 4), QK^T of block n (K slot
-      // n % 4); M(0) skips the PV and M(N) the QK^T.
+      // n % 4); M(0) skips the PV and M(N) the QK^T. slot = n % 4.
       const OperandAddr<C> ad(ln, kring_lds, vring_lds);
-      auto mphase = [&](int n, auto pv, auto qk) {
-        const u32 ks = (u32)((n & 3) * C::TILE_BYTES);
-        const u32 vs = (u32)(((n + 3) & 3) * C::TILE_BYTES);
+      auto mphase = [&](auto slot, auto pv, auto qk) {
+        const u32 ks = (u32)((int)slot * C::TILE_BYTES);
+        const u32 vs = (u32)((((int)slot + 3) & 3) * C::TILE_BYTES);
         matrix_phase<C, decltype(pv)::value, decltype(qk)::value>(ad, ks, vs, qf, pf, s, o);
       };
       constexpr std::true_type on{};
       constexpr std::false_type off{};
+      const int vis4 = vis - 4 * hh;
       // S(n): softmax of block n.
       auto sphase = [&](int n) {
-        const int pos0 = key0 + n * C::BN;
-        if (pos0 + C::BN > wmin) mask_block<C>(s, pos0, vis, hh);
+        int pos0 = key0 + n * C::BN;
+        if (pos0 + C::BN > wmin) {
+          asm volatile("" : "+s"(pos0));  // no per-block induction variables for the rare mask
+          mask_from<C>(s, vis4 - pos0);
+        }
         online_softmax<C>(s, m, l, o, p.scale_log2, pf);
       };
       // Group A: M(n) in phase 2n, S(n) in phase 2n + 1. Group B: S(n - 1)
@@ -547,43 +578,62 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p,
       // phase, group A's during group B's M(N) (when the regions lie in the
       // K ring; else after one more barrier). Straight-line loops per group
       // keep the register assignment of O, S and P fixed across phases; both
-      // groups pass the same number of barriers.
+      // groups pass the same number of barriers. The main loops run four
+      // blocks per iteration (n = 1 mod 4 at its top), so that the ring slots
+      // of every LDS read and DMA are compile-time constants; the remaining
+      // blocks take the general body.
       if (group_a) {
-        if (2 < N) issue_block(2);
-        mphase(0, off, on);
-        __syncthreads();
-        sphase(0);
-        wait_block(1);
-        __syncthreads();
-        for (int n = 1; n < N; ++n) {
-          if (n + 2 < N) issue_block(n + 2);
-          mphase(n, on, on);
+        auto body = [&](int n, auto slot) {
+          if (n + 2 < N) issue_block(n + 2, ((int)slot + 2) & 3);
+          mphase(slot, on, on);
           __syncthreads();
           sphase(n);
           wait_block(n + 1);
           __syncthreads();
+        };
+        if (2 < N) issue_block(2, s2);
+        mphase(s0, off, on);
+        __syncthreads();
+        sphase(0);
+        wait_block(1);
+        __syncthreads();
+        int n = 1;
+        for (; n + 4 <= N; n += 4) {
+          body(n, s1);
+          body(n + 1, s2);
+          body(n + 2, s3);
+          body(n + 3, s0);
         }
-        mphase(N, on, off);
+        for (; n < N; ++n) body(n, n & 3);
+        mphase(N & 3, on, off);
         __syncthreads();
         if constexpr (!kStageInK) __syncthreads();  // group B no longer reads the V ring
         store_output();
       } else {
-        if (2 < N) issue_block(2);
-        __syncthreads();
-        mphase(0, off, on);
-        wait_block(1);
-        __syncthreads();
-        for (int n = 1; n < N; ++n) {
-          if (n + 2 < N) issue_block(n + 2);
+        auto body = [&](int n, auto slot) {
+          if (n + 2 < N) issue_block(n + 2, ((int)slot + 2) & 3);
           sphase(n - 1);
           __syncthreads();
-          mphase(n, on, on);
+          mphase(slot, on, on);
           wait_block(n + 1);
           __syncthreads();
+        };
+        if (2 < N) issue_block(2, s2);
+        __syncthreads();
+        mphase(s0, off, on);
+        wait_block(1);
+        __syncthreads();
+        int n = 1;
+        for (; n + 4 <= N; n += 4) {
+          body(n, s1);
+          body(n + 1, s2);
+          body(n + 2, s3);
+          body(n + 3, s0);
         }
+        for (; n < N; ++n) body(n, n & 3);
         sphase(N - 1);
         __syncthreads();
-        mphase(N, on, off);
+        mphase(N & 3, on, off);
         if constexpr (!kStageInK) __syncthreads();  // every wave's V reads are done
         store_output();
       }
