@@ -743,6 +743,8 @@ def main():
                          big_steps, max(2, args.warmup // 5), big_steps)
     big["workload"] = "Q32768/KV2048 B2H8 D128 BF16 page128 non-causal full cache"
     big["roofline"]["frac_of_vendor_gemm"] = big["roofline"]["achieved"] / gemm
+    big["roofline"]["traffic"] = traffic_from_profile("prefill_direct_q32768")
+    big["roofline"]["traffic_source"] = str(TRAFFIC_SUMMARY.relative_to(ROOT))
     big["steps"] = big_steps
 
     # ---- decode: Q1 / KV32768 -------------------------------------------
