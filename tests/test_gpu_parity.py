@@ -360,6 +360,32 @@ def test_prefill_layout_long_ragged_cache(page):
                          f"prefill long page={page} causal={causal} splits={kern.num_splits}")
 
 
+@pytest.mark.parametrize("dim", [64, 128])
+def test_prefill_layout_every_block_count(dim):
+    """The prefill layout's main loops run four 64-key blocks per iteration
+    and the rest through a general body: requests of 0 to 11 blocks (a partial
+    last block included) take every path, from no block at all through each
+    remainder of the unrolled loop, against the oracle; split 2 halves them."""
+    from fgw_amd.operators.mha.current import build_kernel
+    page, sq = 64, 256
+    lens = [0, 1, 64, 65, 130, 192, 256, 300, 384, 448, 512, 600, 640, 704]
+    width = (max(lens) + page - 1) // page
+    case = (f"blocks_d{dim}", len(lens), sq, 1, dim, page, width)
+    q, k, v, table = O.make_inputs(case, 3, torch.bfloat16)
+    lengths = torch.tensor(lens, dtype=torch.int32)
+    k, v = O.poison_unread(k, v, table, lengths, page)
+    dev = [x.cuda() for x in (q, k, v, table, lengths)]
+    expected = O.reference(q, k, v, table, lengths, page, False)
+    for splits in (None, 2):
+        kern = build_kernel(len(lens), sq, 1, dim, k.shape[0], width, page, False, "bfloat16", 0,
+                            num_splits=splits, layout="prefill")
+        assert kern.layout == "prefill"
+        got = kern(*dev)
+        torch.cuda.synchronize()
+        check_output(got, expected, q, lengths, False,
+                     f"prefill blocks d={dim} splits={kern.num_splits}")
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("dim,page", [(64, 32), (96, 16), (128, 128)])
 def test_prefill_layout_dtypes_and_dims(dtype, dim, page):
