@@ -255,6 +255,8 @@ int64_t fused_merge_counters(const fgw_mha_shape* s, int layout, int splits, int
   (void)rows;
   if (splits < 2 || layout != kLayoutKey || s->sq > 2 || splits > kMergeChunk) return 0;
   if (splits > fused_max_chunk(dim_tile(s->dim))) return 0;
+  // The count travels as int32 (fgw_mha_plan_t.arrival_counters).
+  if (tasks > INT32_MAX / kArrivalStride) return 0;
   return tasks * kArrivalStride;
 }
 

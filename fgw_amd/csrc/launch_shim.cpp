@@ -20,6 +20,7 @@
 #include <cstring>
 #include <map>
 #include <utility>
+#include <vector>
 
 #include "../../include/fgw_mha.h"
 
@@ -112,9 +113,15 @@ int32_t* arrival_counters(int device, hipStream_t stream, int64_t need) {
   if (hipStreamIsCapturing(stream, &status) != hipSuccess || status != hipStreamCaptureStatusNone)
     return nullptr;
   static auto* buffers = new std::map<std::pair<int, uintptr_t>, at::Tensor>();
+  // A buffer replaced by a larger one stays allocated: a kernel still in
+  // flight may be counting in it, and memory the caching allocator handed
+  // to another stream could be written under it.
+  static auto* retired = new std::vector<at::Tensor>();
   at::Tensor& buf = (*buffers)[{device, reinterpret_cast<uintptr_t>(stream)}];
-  if (!buf.defined() || buf.numel() < need)
+  if (!buf.defined() || buf.numel() < need) {
+    if (buf.defined()) retired->push_back(buf);
     buf = at::zeros({need}, at::TensorOptions().device(c10::kCUDA, device).dtype(at::kInt));
+  }
   return static_cast<int32_t*>(buf.data_ptr());
 }
 
