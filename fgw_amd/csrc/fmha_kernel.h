@@ -230,6 +230,19 @@ __device__ __forceinline__ u32 lds_address(const void* p) {
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ u32 uniform_u32(u32 x) { return __builtin_amdgcn_readfirstlane(x); }
+
+// Values the compiler cannot see through (uniform, and per lane): code derived
+// from them stays where it is written, in a cold branch or once per work item,
+// instead of being hoisted out of the work-item loop and held in registers
+// across the main loop.
+__device__ __forceinline__ int opaque_uniform(int x) {
+  asm volatile("" : "+s"(x));
+  return x;
+}
+__device__ __forceinline__ int opaque_lane(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
 // Uniform global base + per-lane 32-bit offset (saddr form).
 __device__ __forceinline__ void dma_saddr(const void* base, u32 voff, u32 lds) {
   const uint64_t b = (uint64_t)base;

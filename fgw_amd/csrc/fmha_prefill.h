@@ -169,6 +169,8 @@ __device__ __forceinline__ void issue_slow_tile(const FwdParams& p, const int32_
                                                 const char* base, int64_t row_bytes, int pos0,
                                                 int len, u32 dst, int wave, int lane) {
   const u32 page = (u32)p.page_size;
+  const int dim = opaque_uniform(p.dim);
+  lane = opaque_lane(lane);
   const char* zero = reinterpret_cast<const char*>(kZeroChunk);
 #pragma unroll
   for (int q = 0; q < C::INSTR_PER_WAVE; ++q) {
@@ -180,7 +182,7 @@ __device__ __forceinline__ void issue_slow_tile(const FwdParams& p, const int32_
     const int64_t row = (int64_t)id * page + ((u32)pos - pg * page);
     const bool live = pos < len && id >= 0 && row < p.pool_rows;
     const int c = IS_V ? pos_in_row ^ (4 * (r % C::VSW)) : pos_in_row ^ (r % C::KSW);
-    const char* src = live && c * 8 < p.dim ? base + row * row_bytes + c * 16 : zero;
+    const char* src = live && c * 8 < dim ? base + row * row_bytes + c * 16 : zero;
     dma_flat(src, dst + 1024u * i);
   }
 }
@@ -307,17 +309,23 @@ __device__ __forceinline__ void matrix_phase(const OperandAddr<C>& ad, u32 koff,
 // Scores of keys at or beyond the lane's visible count become -inf: element
 // (t, v) holds key pos0 + 4 (lane / 32) + 32 t + 8 (v / 4) + v % 4, masked
 // when 32 t + 8 (v / 4) + v % 4 >= lim = vis - 4 (lane / 32) - pos0.
+// Each compare feeds its select right away (the fence): the compiler would
+// otherwise issue all 32 compares first and hold their lane masks in 64
+// scalar registers, which made the kernel spill scalars around the main loop.
 template <class C>
 __device__ __forceinline__ void mask_from(f32x16 (&s)[C::ST], int lim) {
 #pragma unroll
   for (int t = 0; t < C::ST; ++t)
 #pragma unroll
-    for (int v = 0; v < 16; ++v)
-      if (32 * t + 8 * (v >> 2) + (v & 3) >= lim) s[t][v] = -INFINITY;
+    for (int v = 0; v < 16; ++v) {
+      const int idx = 32 * t + 8 * (v >> 2) + (v & 3);
+      s[t][v] = idx >= lim ? -INFINITY : s[t][v];
+      __builtin_amdgcn_sched_barrier(0);
+    }
 }
 
 template <class C>
-__global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p,
+__global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p_arg,
                                                              const int32_t* __restrict__ table,
                                                              const int32_t* __restrict__ lengths) {
   __shared__ __attribute__((aligned(1024))) unsigned char smem[C::LDS_BYTES];
@@ -327,9 +335,20 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p,
   const u32 kring_lds = lds_address(kring);
   const u32 vring_lds = kring_lds + (u32)(C::NKSLOT * C::TILE_BYTES);
 
+  // The parameters. The work items read them again from the kernel argument
+  // segment (p_arg is its first argument, at offset 0) through a pointer the
+  // compiler cannot follow: it then loads what each item and each output
+  // store needs where they need it, instead of holding every parameter (and
+  // what it derives from them) in scalar registers across the main loop.
+  const FwdParams& p = p_arg;
+  auto kernarg = []() {
+    typedef const __attribute__((address_space(4))) FwdParams* KP;
+    KP kp = (KP)__builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(kp));
+    return (const FwdParams*)kp;
+  };
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const bool group_a = wave < C::WAVES / 2;
   const int lane = tid & 63;
   const int il = lane & 31, hh = lane >> 5;
   const Lanes<C> ln(lane);
@@ -355,6 +374,8 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p,
   const int capacity = p.width * p.page_size;
 
   for (int it = 0; it < count; ++it) {
+    const FwdParams p = *kernarg();  // this item's copy (shadows the prologue's reference)
+    const bool group_a = opaque_uniform(wave) < C::WAVES / 2;
     int w = a + local + nx * it;
     int split, nsplit = p.splits, qt, h, b;
     if (p.split_keys > 0) {
@@ -411,13 +432,14 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p,
     int32_t id_first = block_page_id<C>(p, table_b, key0_full, lane);
     u32x4 qf[C::KK];
     {
+      const int dim = opaque_uniform(p.dim), hq = opaque_lane(hh);
       const u16* qp =
           static_cast<const u16*>(p.q) + (((int64_t)b * p.sq + qrow) * p.heads + h) * p.dim;
 #pragma unroll
       for (int kk = 0; kk < C::KK; ++kk) {
-        const int d = 16 * kk + 8 * hh;
+        const int d = 16 * kk + 8 * hq;
         u32x4 val = {0u, 0u, 0u, 0u};
-        if (qrow < p.sq && d < p.dim)
+        if (qrow < p.sq && d < dim)
           val = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(qp + d));
         qf[kk] = val;
       }
@@ -454,41 +476,45 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p,
     // that region meanwhile. kStageInK: the eight regions lie in the K ring
     // (head-dim tile 128; at 64 the upper four reach into the V ring).
     constexpr bool kStageInK = C::WAVES * 32 * kStagedRowBytes<C> <= C::NKSLOT * C::TILE_BYTES;
-    // Partials, unless a one-split tile of a tile-balanced whole call writes
-    // its output rows directly.
-    const bool to_parts = p.mode == 1 && !(p.split_direct && nsplit == 1);
     auto store_output = [&]() {
+      // The output's parameters come from the kernel arguments again here,
+      // so that none of them is held in a register across the main loop.
+      const FwdParams po = *kernarg();
+      // Partials, unless a one-split tile of a tile-balanced whole call
+      // writes its output rows directly.
+      const bool to_parts = po.mode == 1 && !(po.split_direct && nsplit == 1);
+      const int ho = opaque_lane(hh), qr = row_base + opaque_lane(il);
       const float tot = pair_sum(l);
-      if (p.dim == C::DPAD) {
+      if (po.dim == C::DPAD) {
         static_assert(C::WAVES * 32 * kStagedRowBytes<C> <= C::LDS_BYTES, "staged rows fit");
         const bool f32 = to_parts;
-        float* fdst =
-            f32 ? p.parts + ((((int64_t)b * p.heads + h) * p.splits + split) * p.sq + row_base) *
-                                C::DPAD
-                : nullptr;
+        float* fdst = f32 ? po.parts + ((((int64_t)b * po.heads + h) * po.splits + split) * po.sq +
+                                        row_base) *
+                                           C::DPAD
+                          : nullptr;
         unsigned char* bdst =
             f32 ? nullptr
-                : static_cast<unsigned char*>(p.out) +
-                      (((int64_t)b * p.sq + row_base) * p.heads + h) * C::DPAD * 2;
+                : static_cast<unsigned char*>(po.out) +
+                      (((int64_t)b * po.sq + row_base) * po.heads + h) * C::DPAD * 2;
         store_rows_staged<C>(smem + wave * 32 * kStagedRowBytes<C>, lane, o,
                              1.0f / fmaxf(tot, 1.0e-30f), f32, fdst, bdst,
-                             (int64_t)p.heads * C::DPAD * 2, p.sq - row_base);
-        if (to_parts && hh == 0 && qrow < p.sq)
-          p.lse[(((int64_t)b * p.heads + h) * p.splits + split) * p.sq + qrow] = lse_of(m, tot);
-      } else if (qrow < p.sq) {
+                             (int64_t)po.heads * C::DPAD * 2, po.sq - row_base);
+        if (to_parts && ho == 0 && qr < po.sq)
+          po.lse[(((int64_t)b * po.heads + h) * po.splits + split) * po.sq + qr] = lse_of(m, tot);
+      } else if (qr < po.sq) {
         const float inv = 1.0f / fmaxf(tot, 1.0e-30f);
 #pragma unroll
         for (int dt = 0; dt < C::DT; ++dt)
 #pragma unroll
           for (int gq = 0; gq < 4; ++gq) {
-            const int d0 = 32 * dt + 8 * gq + 4 * hh;
-            if (d0 < p.dim) {
+            const int d0 = 32 * dt + 8 * gq + 4 * ho;
+            if (d0 < po.dim) {
               f32x4 val = {o[dt][4 * gq], o[dt][4 * gq + 1], o[dt][4 * gq + 2], o[dt][4 * gq + 3]};
-              store_row<C>(p, b, h, split, qrow, d0, val, inv, -1, 0, to_parts ? 1 : 0);
+              store_row<C>(po, b, h, split, qr, d0, val, inv, -1, 0, to_parts ? 1 : 0);
             }
           }
-        if (to_parts && hh == 0) {
-          p.lse[(((int64_t)b * p.heads + h) * p.splits + split) * p.sq + qrow] = lse_of(m, tot);
+        if (to_parts && ho == 0) {
+          po.lse[(((int64_t)b * po.heads + h) * po.splits + split) * po.sq + qr] = lse_of(m, tot);
         }
       }
     };
