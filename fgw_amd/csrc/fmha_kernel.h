@@ -332,7 +332,11 @@ template <class C, bool IS_V>
 __device__ __forceinline__ void issue_tile(const FwdParams& p, const DmaLanes<C>& dl,
                                            const int32_t* table_b, const char* base,
                                            int64_t row_bytes, int pos0, int32_t id0, int len,
-                                           unsigned char* dst, int wq, int lane) {
+                                           unsigned char* dst_ptr, int wq, int lane) {
+  // The LDS destination through an opaque copy: the compiler would otherwise
+  // precompute every instruction's destination for every stage once and
+  // hold them all in scalar registers across the work-item loop.
+  const u32 dst = (u32)opaque_uniform((int)lds_address(dst_ptr));
   const u32 page = (u32)p.page_size;
   const u32 pg0 = div_page((u32)pos0, p.page_magic, p.page_shift);
   const u32 off0 = (u32)pos0 - pg0 * page;
@@ -345,10 +349,13 @@ __device__ __forceinline__ void issue_tile(const FwdParams& p, const DmaLanes<C>
       const int i = q * C::NWQ + wq;
       const int64_t rb = (row0 + C::RPI * i) * row_bytes;
       const u32 off = IS_V ? dl.vq(q, wq) : dl.kq(q, wq);
-      __builtin_amdgcn_global_load_lds(base + rb + off, FGW_LDS(void, dst + 1024 * i), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(base + rb + off, FGW_LDS(void, (uintptr_t)(dst + 1024u * i)),
+                                       16, 0, 0);
     }
     return;
   }
+  const int dim = opaque_uniform(p.dim);
+  lane = opaque_lane(lane);
   const char* zero = reinterpret_cast<const char*>(kZeroChunk);
   int32_t ids[C::INSTR_PER_WAVE];
 #pragma unroll
@@ -366,8 +373,8 @@ __device__ __forceinline__ void issue_tile(const FwdParams& p, const DmaLanes<C>
     const int64_t row = (int64_t)ids[q] * page + ((u32)pos - pg * page);
     const bool live = pos < len && row >= 0 && row < p.pool_rows;
     const int c = IS_V ? pos_in_row ^ (4 * (r % C::VSW)) : pos_in_row ^ (r % C::KSW);
-    const char* src = live && c * 8 < p.dim ? base + row * row_bytes + c * 16 : zero;
-    __builtin_amdgcn_global_load_lds(src, FGW_LDS(void, dst + 1024 * i), 16, 0, 0);
+    const char* src = live && c * 8 < dim ? base + row * row_bytes + c * 16 : zero;
+    __builtin_amdgcn_global_load_lds(src, FGW_LDS(void, (uintptr_t)(dst + 1024u * i)), 16, 0, 0);
   }
 }
 
@@ -439,7 +446,9 @@ __device__ __forceinline__ void qk_block(const unsigned char* kt, const Lanes<C>
   }
 }
 
-// Scores of keys at or beyond the lane's visible count become -inf.
+// Scores of keys at or beyond the lane's visible count become -inf. Each
+// compare feeds its select right away (the fence), so that the compiler does
+// not hold 32 lane masks in scalar registers at once.
 template <class C>
 __device__ __forceinline__ void mask_block(f32x16 (&s)[C::ST], int pos0, int vis, int hh) {
 #pragma unroll
@@ -447,7 +456,8 @@ __device__ __forceinline__ void mask_block(f32x16 (&s)[C::ST], int pos0, int vis
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
       const int key = pos0 + 32 * t + 8 * (v >> 2) + 4 * hh + (v & 3);
-      if (key >= vis) s[t][v] = -INFINITY;
+      s[t][v] = key >= vis ? -INFINITY : s[t][v];
+      __builtin_amdgcn_sched_barrier(0);
     }
 }
 
@@ -998,7 +1008,7 @@ __device__ void arrive_and_merge(const FwdParams& p, int b, int h, int qt, int u
   __syncthreads();  // ... and every wave's
   int* flag = reinterpret_cast<int*>(lds);
   int32_t* ctr = p.arrivals + (((int64_t)b * p.heads + h) * p.q_tiles + qt) * kArrivalStride;
-  if (tid == 0) {
+  if (opaque_lane(tid) == 0) {
     const int prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     *flag = prev == used - 1;
   }
@@ -1027,10 +1037,23 @@ __device__ __forceinline__ int32_t page_id(const FwdParams& p, const int32_t* ta
 // table and lengths come as separate read-only, non-aliasing arguments so
 // that uniform reads of them can use the scalar cache.
 template <class C>
-__global__ __launch_bounds__(C::THREADS) void fwd_kernel(FwdParams p,
+__global__ __launch_bounds__(C::THREADS) void fwd_kernel(FwdParams p_arg,
                                                          const int32_t* __restrict__ table,
                                                          const int32_t* __restrict__ lengths) {
   __shared__ __attribute__((aligned(1024))) unsigned char smem[C::LDS_BYTES];
+  // The parameters. Each work item reads them again from the kernel argument
+  // segment (p_arg is its first argument, at offset 0) through a pointer the
+  // compiler cannot follow, once for its set-up and main loop and once for
+  // its output: it then loads what each part needs where it needs it,
+  // instead of holding every parameter (and what it derives from them) in
+  // scalar registers across the main loop.
+  const FwdParams& p = p_arg;
+  auto kernarg = []() {
+    typedef const __attribute__((address_space(4))) FwdParams* KP;
+    KP kp = (KP)__builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(kp));
+    return (const FwdParams*)kp;
+  };
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1078,6 +1101,12 @@ __global__ __launch_bounds__(C::THREADS) void fwd_kernel(FwdParams p,
   }
 
   for (int it = 0; it < count; ++it) {
+    // This item's copy of the parameters and of the values derived from them
+    // above (they shadow the set-up's).
+    FwdParams p = *kernarg();
+    const int capacity = p.width * p.page_size;
+    const int tasks = p.batch * p.heads * p.q_tiles;
+    const bool balanced = C::LAYOUT == kLayoutKey && p.mode == 1 && p.split_keys > 0;
     int w = first + it, split = 0, slot = -1, seg_lo = 0, seg_hi = 0, nsplit = p.splits;
     if (p.mode == 2) {
       const int32_t* sg = p.segs + 4 * (int64_t)w;
@@ -1179,13 +1208,14 @@ __global__ __launch_bounds__(C::THREADS) void fwd_kernel(FwdParams p,
     // Q after the first DMA: its loads overlap the tile's.
     u32x4 qf[C::KK];
     {
+      const int dim = opaque_uniform(p.dim), hq = opaque_lane(hh);
       const u16* qp =
           static_cast<const u16*>(p.q) + (((int64_t)b * p.sq + qrow) * p.heads + h) * p.dim;
 #pragma unroll
       for (int kk = 0; kk < C::KK; ++kk) {
-        const int d = 16 * kk + 8 * hh;
+        const int d = 16 * kk + 8 * hq;
         u32x4 val = {0u, 0u, 0u, 0u};
-        if (qrow < p.sq && d < p.dim) val = load16(qp + d);
+        if (qrow < p.sq && d < dim) val = load16(qp + d);
         qf[kk] = val;
       }
     }
@@ -1219,6 +1249,7 @@ __global__ __launch_bounds__(C::THREADS) void fwd_kernel(FwdParams p,
     }
 
     wait_dma();  // no DMA of this work item outlives it
+    p = *kernarg();  // the output's parameters, not held across the main loop
     if constexpr (C::NWK == 1) {
       const float tot = pair_sum(l);
       // Direct stores: D < DPAD, or D tiles below 128 (staged, D tile 64
@@ -1226,11 +1257,12 @@ __global__ __launch_bounds__(C::THREADS) void fwd_kernel(FwdParams p,
       auto store_direct = [&]() {
         if (qrow >= p.sq) return;
         const float inv = 1.0f / fmaxf(tot, 1.0e-30f);
+        const int ho = opaque_lane(hh);
 #pragma unroll
         for (int dt = 0; dt < C::DT; ++dt)
 #pragma unroll
           for (int gq = 0; gq < 4; ++gq) {
-            const int d0 = 32 * dt + 8 * gq + 4 * hh;
+            const int d0 = 32 * dt + 8 * gq + 4 * ho;
             if (d0 < p.dim) {
               f32x4 val = {o[dt][4 * gq], o[dt][4 * gq + 1], o[dt][4 * gq + 2], o[dt][4 * gq + 3]};
               store_row<C>(p, b, h, split, qrow, d0, val, inv, slot, q0);
