@@ -55,7 +55,10 @@
 //
 // Q is loaded and O stored with non-temporal hints: each is touched once,
 // while the K/V blocks of (b, h) are read again by its other query tiles
-// from the L2.
+// from the L2. A program with another work item to come prefetches that
+// item's Q rows into the L2 before its last blocks (after the four-block
+// main loop), so that the next item's Q loads do not queue at HBM behind
+// those of every other program.
 #pragma once
 #include <utility>
 
@@ -97,7 +100,10 @@ struct PCfg {
   static constexpr int TILE_BYTES = BN * ROW_BYTES;
   static constexpr int NKSLOT = 4;
   static constexpr int NVSLOT = 4;
-  static constexpr int LDS_BYTES = (NKSLOT + NVSLOT) * TILE_BYTES;
+  static constexpr int RING_BYTES = (NKSLOT + NVSLOT) * TILE_BYTES;
+  // After the rings: 1 KB per wave that the L2 prefetch of the next work
+  // item's Q rows writes and nothing reads.
+  static constexpr int LDS_BYTES = RING_BYTES + 1024 * WAVES;
   static constexpr int INSTR = TILE_BYTES / 1024;  // DMA instructions per tile
   static constexpr int INSTR_PER_WAVE = INSTR / NWQ;
   static constexpr int BATCH = 2 * INSTR_PER_WAVE;  // per wave: its share of one K and one V tile
@@ -373,11 +379,10 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p_arg,
   const int count = local < end - a ? (end - a - local + nx - 1) / nx : 0;
   const int capacity = p.width * p.page_size;
 
-  for (int it = 0; it < count; ++it) {
-    const FwdParams p = *kernarg();  // this item's copy (shadows the prologue's reference)
-    const bool group_a = opaque_uniform(wave) < C::WAVES / 2;
-    int w = a + local + nx * it;
-    int split, nsplit = p.splits, qt, h, b;
+  // Work item w: (b, h, query tile qt, split of nsplit).
+  auto decode = [&](const FwdParams& p, int w, int& b, int& h, int& qt, int& split,
+                    int& nsplit) {
+    nsplit = p.splits;
     if (p.split_keys > 0) {
       // Tile-balanced causal plan: the items of one (b, h) are contiguous
       // (a program's range, and with the XCD remap one XCD's, shares its K/V
@@ -408,6 +413,13 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p_arg,
       h = w % p.heads;
       b = w / p.heads;
     }
+  };
+
+  for (int it = 0; it < count; ++it) {
+    const FwdParams p = *kernarg();  // this item's copy (shadows the prologue's reference)
+    const bool group_a = opaque_uniform(wave) < C::WAVES / 2;
+    int split, nsplit, qt, h, b;
+    decode(p, a + local + nx * it, b, h, qt, split, nsplit);
     const int32_t* table_b = table + (int64_t)b * p.width;
     const char* kb = static_cast<const char*>(p.k) + (int64_t)h * p.dim * 2;
     const char* vb = static_cast<const char*>(p.v) + (int64_t)h * p.dim * 2;
@@ -486,7 +498,7 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p_arg,
       const int ho = opaque_lane(hh), qr = row_base + opaque_lane(il);
       const float tot = pair_sum(l);
       if (po.dim == C::DPAD) {
-        static_assert(C::WAVES * 32 * kStagedRowBytes<C> <= C::LDS_BYTES, "staged rows fit");
+        static_assert(C::WAVES * 32 * kStagedRowBytes<C> <= C::RING_BYTES, "staged rows fit");
         const bool f32 = to_parts;
         float* fdst = f32 ? po.parts + ((((int64_t)b * po.heads + h) * po.splits + split) * po.sq +
                                         row_base) *
@@ -560,6 +572,36 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p_arg,
         else
           wait_vm<0>();
       };
+      // L2 prefetch of the next item's Q rows, issued by every wave after the
+      // four-block main loop, before the remaining blocks: one LDS DMA per
+      // wave (into its scratch kilobyte after the rings) whose 64 lanes touch
+      // the 64 lines of the wave's next Q rows, so that the next item's Q
+      // loads hit L2 instead of queueing at HBM behind those of every other
+      // program. The first remaining body's wait leaves it in flight behind
+      // that body's batch; the next wait covers it.
+      const bool pf_on = it + 1 < count;
+      auto prefetch = [&]() {
+        const FwdParams& p = *kernarg();
+        int bn, hn, qtn, splitn, nsplitn;
+        decode(p, a + local + nx * (it + 1), bn, hn, qtn, splitn, nsplitn);
+        const int row = qtn * C::ROWS_TILE + wave * C::ROWS_WAVE + il;
+        const int rc = row < p.sq ? row : p.sq - 1;
+        const char* addr = static_cast<const char*>(p.q) +
+                           (((int64_t)bn * p.sq + rc) * p.heads + hn) * p.dim * 2 +
+                           (hh * 128 < p.dim * 2 ? hh * 128 : 0);
+        dma_flat(addr, kring_lds + (u32)(C::RING_BYTES + 1024 * wave));
+      };
+      // The wait at the end of body(n): block n + 1 has landed. After the
+      // prefetch (pf_wait) the batch of block n + 2, when there is one, and
+      // the prefetch may stay in flight.
+      auto wait_body = [&](int n, bool pf_wait) {
+        if (!pf_wait)
+          wait_block(n + 1);
+        else if (n + 2 < N)
+          wait_vm<C::BATCH + 1>();
+        else
+          wait_vm<1>();
+      };
       constexpr std::integral_constant<int, 0> s0{};
       constexpr std::integral_constant<int, 1> s1{};
       constexpr std::integral_constant<int, 2> s2{};
@@ -615,12 +657,12 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p_arg,
       // of every LDS read and DMA are compile-time constants; the remaining
       // blocks take the general body.
       if (group_a) {
-        auto body = [&](int n, auto slot) {
+        auto body = [&](int n, auto slot, bool pf_wait = false) {
           if (n + 2 < N) issue_block(n + 2, ((int)slot + 2) & 3);
           mphase(slot, on, on);
           __syncthreads();
           sphase(n);
-          wait_block(n + 1);
+          wait_body(n, pf_wait);
           __syncthreads();
         };
         if (2 < N) issue_block(2, s2);
@@ -636,18 +678,20 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p_arg,
           body(n + 2, s3);
           body(n + 3, s0);
         }
-        for (; n < N; ++n) body(n, n & 3);
+        if (pf_on) prefetch();
+        const int n_rem = n;
+        for (; n < N; ++n) body(n, n & 3, pf_on && n == n_rem);
         mphase(N & 3, on, off);
         __syncthreads();
         if constexpr (!kStageInK) __syncthreads();  // group B no longer reads the V ring
         store_output();
       } else {
-        auto body = [&](int n, auto slot) {
+        auto body = [&](int n, auto slot, bool pf_wait = false) {
           if (n + 2 < N) issue_block(n + 2, ((int)slot + 2) & 3);
           sphase(n - 1);
           __syncthreads();
           mphase(slot, on, on);
-          wait_block(n + 1);
+          wait_body(n, pf_wait);
           __syncthreads();
         };
         if (2 < N) issue_block(2, s2);
@@ -662,7 +706,9 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p_arg,
           body(n + 2, s3);
           body(n + 3, s0);
         }
-        for (; n < N; ++n) body(n, n & 3);
+        if (pf_on) prefetch();
+        const int n_rem = n;
+        for (; n < N; ++n) body(n, n & 3, pf_on && n == n_rem);
         sphase(N - 1);
         __syncthreads();
         mphase(N & 3, on, off);

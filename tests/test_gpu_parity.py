@@ -365,7 +365,10 @@ def test_prefill_layout_every_block_count(dim):
     """The prefill layout's main loops run four 64-key blocks per iteration
     and the rest through a general body: requests of 0 to 11 blocks (a partial
     last block included) take every path, from no block at all through each
-    remainder of the unrolled loop, against the oracle; split 2 halves them."""
+    remainder of the unrolled loop, against the oracle; split 2 halves them.
+    Persistent grids of 1 and 3 programs run the items back to back, so that
+    every program prefetches its next item's Q rows from each of those
+    paths: bit-identical to one program per item."""
     from fgw_amd.operators.mha.current import build_kernel
     page, sq = 64, 256
     lens = [0, 1, 64, 65, 130, 192, 256, 300, 384, 448, 512, 600, 640, 704]
@@ -377,13 +380,20 @@ def test_prefill_layout_every_block_count(dim):
     dev = [x.cuda() for x in (q, k, v, table, lengths)]
     expected = O.reference(q, k, v, table, lengths, page, False)
     for splits in (None, 2):
-        kern = build_kernel(len(lens), sq, 1, dim, k.shape[0], width, page, False, "bfloat16", 0,
-                            num_splits=splits, layout="prefill")
-        assert kern.layout == "prefill"
-        got = kern(*dev)
-        torch.cuda.synchronize()
-        check_output(got, expected, q, lengths, False,
-                     f"prefill blocks d={dim} splits={kern.num_splits}")
+        first = None
+        for persistent in (None, 1, 3):
+            kern = build_kernel(len(lens), sq, 1, dim, k.shape[0], width, page, False, "bfloat16",
+                                0, num_splits=splits, layout="prefill",
+                                persistent_programs=persistent)
+            assert kern.layout == "prefill"
+            got = kern(*dev)
+            torch.cuda.synchronize()
+            check_output(got, expected, q, lengths, False,
+                         f"prefill blocks d={dim} splits={kern.num_splits} grid={kern.compute_grid}")
+            if first is None:
+                first = got
+            else:
+                assert torch.equal(got, first), f"grid {kern.compute_grid} changed the output"
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
