@@ -443,7 +443,11 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p_arg,
     const int key0_full = first_block(capacity) * C::BN;
     int32_t id_first = block_page_id<C>(p, table_b, key0_full, lane);
     u32x4 qf[C::KK];
-    {
+    // A program's first item, a whole query tile at D == DPAD, reads Q
+    // through LDS (below, after the item-top barrier); the others load their
+    // rows straight into registers (from the L2, after the prefetch).
+    const bool q_lds = it == 0 && q0 + C::ROWS_TILE <= p.sq && p.dim == C::DPAD;
+    if (!q_lds) {
       const int dim = opaque_uniform(p.dim), hq = opaque_lane(hh);
       const u16* qp =
           static_cast<const u16*>(p.q) + (((int64_t)b * p.sq + qrow) * p.heads + h) * p.dim;
@@ -538,6 +542,7 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p_arg,
       // following window is read one window ahead.
       // Each branch consumes its own page-id load, so the common one (the
       // guess held) waits only for that load and not for Q behind it.
+      const OperandAddr<C> ad_q(ln, kring_lds, vring_lds);
       BlockWindow win0{0, 0};
       if (key0 == key0_full)
         win0.off = block_offset_of<C>(p, id_first, row_bytes, key0, N, len, lane);
@@ -606,13 +611,51 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p_arg,
       constexpr std::integral_constant<int, 1> s1{};
       constexpr std::integral_constant<int, 2> s2{};
       constexpr std::integral_constant<int, 3> s3{};
+      // Q through LDS: its four 64-row tiles in the way of K tiles (the rows
+      // of Q and of the pool have the same stride, H D elements: 4 full rows
+      // per instruction instead of 32 B of 32 rows), into K slots 2, 3 and V
+      // slots 2, 3, which blocks 2 and 3 fill only after the barrier before
+      // M(0); each wave then reads its 32 rows with the K operand addresses.
+      if (q_lds) {
+        // (opaque copies: nothing of this once-per-program path is held
+        // across the main loop)
+        const int wv = opaque_uniform(wave);
+        int64_t rb = row_bytes;
+        asm volatile("" : "+s"(rb));
+        const int64_t tile_q = 64 * rb;
+        const char* qb = static_cast<const char*>(p.q) +
+                         (((int64_t)b * p.sq + q0) * p.heads + h) * p.dim * 2;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const u32 dst = (j < 2 ? kring_lds : vring_lds) + (u32)((2 + (j & 1)) * C::TILE_BYTES) +
+                          1024u * (u32)wv;
+#pragma unroll
+          for (int q = 0; q < C::INSTR_PER_WAVE; ++q)
+            dma_saddr(qb + j * tile_q, bd.k[q], dst + 1024u * (u32)(q * C::NWQ));
+        }
+      }
       issue_block(0, s0);
       if (1 < N) issue_block(1, s1);
+      if (q_lds) {
+        // Q has landed (its loads are older than blocks 0 and 1), in every
+        // wave.
+        if (1 < N)
+          wait_vm<2 * C::BATCH>();
+        else
+          wait_vm<C::BATCH>();
+        __syncthreads();
+        const int wv = opaque_uniform(wave), j = wv >> 1, t = wv & 1;
+        const u32 off = (u32)((j < 2 ? 2 + j : 6 + (j - 2)) * C::TILE_BYTES + t * 32 * C::ROW_BYTES);
+#pragma unroll
+        for (int kk = 0; kk < C::KK; ++kk)
+          qf[kk] = *(const __attribute__((address_space(3))) u32x4*)(lds_at(ad_q.k[kk]) + off);
+      }
 
       win1.off = block_offset<C>(p, table_b, row_bytes, key0, N, len, 64 + lane);
       wait_block(0);
-      // Q has landed too (its loads are older than block 0's). The empty
-      // assembly makes the compiler wait for them here, once, instead of
+      // Q has landed too (its register loads are older than block 0's; its
+      // LDS reads, on the LDS path, complete here). The empty assembly makes
+      // the compiler wait for them here, once, instead of
       // before the first QK^T MFMA of every matrix phase, where its vmcnt(0)
       // would also wait for the DMA batch in flight.
 #pragma unroll
