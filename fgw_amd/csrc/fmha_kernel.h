@@ -614,12 +614,46 @@ __device__ __forceinline__ void store_row(const FwdParams& p, int b, int h, int 
 template <class C>
 constexpr int kStagedRowBytes = 2 * C::DPAD > 256 ? 2 * C::DPAD : 256;
 
+// bf16/fp16 staging (D == DPAD): lane (il, hh) writes its part of row il,
+// scaled by inv, into the wave's region `st`.
+template <class C>
+__device__ __forceinline__ void write_staged_bf16(unsigned char* st, int il, int hh,
+                                                  const f32x16 (&o)[C::DT], float inv) {
+  using E = Elem<C::BF16>;
+  constexpr int RB = C::DPAD * 2, NCH = RB / 16;
+#pragma unroll
+  for (int dt = 0; dt < C::DT; ++dt)
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) {
+      const int c = 4 * dt + gq;
+      u32x2 w;
+      w.x = E::pack2(o[dt][4 * gq] * inv, o[dt][4 * gq + 1] * inv);
+      w.y = E::pack2(o[dt][4 * gq + 2] * inv, o[dt][4 * gq + 3] * inv);
+      *reinterpret_cast<u32x2*>(st + il * RB + 16 * (c ^ (il % NCH)) + 8 * hh) = w;
+    }
+  __builtin_amdgcn_wave_barrier();
+}
+
+// 16-byte read-backs per lane for the wave's 32 staged bf16/fp16 rows.
+template <class C>
+constexpr int kStagedChunks = C::DPAD / 16;
+
+// Read-back k (0 <= k < kStagedChunks) of a lane: 16-byte chunk lane % NCH
+// of staged bf16/fp16 row RPI k + lane / NCH (NCH = DPAD / 8 chunks per
+// row, RPI = 64 / NCH rows per instruction).
+template <class C>
+__device__ __forceinline__ u32x4 read_staged_bf16(const unsigned char* st, int lane, int k) {
+  constexpr int RB = C::DPAD * 2, NCH = RB / 16, RPI = 64 / NCH;
+  static_assert(32 / RPI == kStagedChunks<C>, "read-backs per lane");
+  const int r = RPI * k + lane / NCH, c = lane % NCH;
+  return *reinterpret_cast<const u32x4*>(st + r * RB + 16 * (c ^ (r % NCH)));
+}
+
 template <class C>
 __device__ __forceinline__ void store_rows_staged(unsigned char* st, int lane,
                                                   const f32x16 (&o)[C::DT], float inv, bool f32,
                                                   float* fdst, unsigned char* bdst,
                                                   int64_t brow_stride, int rows) {
-  using E = Elem<C::BF16>;
   static_assert(C::DPAD >= 64 && C::DPAD % 64 == 0, "staged rows need D tiles of 64k");
   // The lane id passes through an opaque copy so that the compiler cannot
   // hoist the staging addresses (functions of the lane alone) out of the
@@ -649,22 +683,12 @@ __device__ __forceinline__ void store_rows_staged(unsigned char* st, int lane,
       __builtin_amdgcn_wave_barrier();  // the next pass rewrites the region
     }
   } else {
-    constexpr int RB = C::DPAD * 2, NCH = RB / 16, RPI = 64 / NCH;
+    constexpr int NCH = C::DPAD * 2 / 16, RPI = 64 / NCH;
+    write_staged_bf16<C>(st, il, hh, o, inv);
 #pragma unroll
-    for (int dt = 0; dt < C::DT; ++dt)
-#pragma unroll
-      for (int gq = 0; gq < 4; ++gq) {
-        const int c = 4 * dt + gq;
-        u32x2 w;
-        w.x = E::pack2(o[dt][4 * gq] * inv, o[dt][4 * gq + 1] * inv);
-        w.y = E::pack2(o[dt][4 * gq + 2] * inv, o[dt][4 * gq + 3] * inv);
-        *reinterpret_cast<u32x2*>(st + il * RB + 16 * (c ^ (il % NCH)) + 8 * hh) = w;
-      }
-    __builtin_amdgcn_wave_barrier();
-#pragma unroll
-    for (int k = 0; k < 32 / RPI; ++k) {
+    for (int k = 0; k < kStagedChunks<C>; ++k) {
       const int r = RPI * k + lane / NCH, c = lane % NCH;
-      const u32x4 v = *reinterpret_cast<const u32x4*>(st + r * RB + 16 * (c ^ (r % NCH)));
+      const u32x4 v = read_staged_bf16<C>(st, lane, k);
       if (r < rows)
         __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(bdst + r * brow_stride + 16 * c));
     }
@@ -1069,7 +1093,6 @@ __global__ __launch_bounds__(C::THREADS) void fwd_kernel(FwdParams p_arg,
   const int grid = gridDim.x;
   const int prog = xcd_remap(blockIdx.x, grid);
   const int capacity = p.width * p.page_size;
-  const int tasks = p.batch * p.heads * p.q_tiles;
   // Length-balanced splits (key layout, partial mode): request b takes
   // pre[b + 1] - pre[b] splits; its work items are [pre[b], pre[b + 1]) x
   // H x q_tiles, split-major (see the decode of w below).

@@ -415,6 +415,30 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p_arg,
     }
   };
 
+  // Deferred output rows. A wave's last stores of an item would sit in the
+  // vector memory counter ahead of the next item's first DMA (the counter
+  // retires loads and stores in issue order), so the waits for that item's
+  // blocks 0 and 1 would wait for them too. When another item follows, a
+  // wave with all 32 of its rows in bf16/fp16 output stages them, keeps
+  // them in dfr and stores them right after the next item's DMA of blocks 0
+  // and 1; those two waits leave them in flight, and the wait for block 2
+  // (or the last one) covers them. The address and step are held per lane,
+  // and a zero step means nothing pending.
+  constexpr int kRowChunks = C::DPAD * 2 / 16, kRowsPerStore = 64 / kRowChunks;
+  constexpr int kDefer = kStagedChunks<C>;  // stores per lane
+  u32x4 dfr[kDefer];
+  uint64_t dfr_addr = 0;
+  int dfr_step = 0;
+  auto store_deferred = [&]() {
+#pragma unroll
+    for (int k = 0; k < kDefer; ++k)
+      __builtin_nontemporal_store(
+          dfr[k], reinterpret_cast<u32x4*>(dfr_addr + (uint64_t)(int64_t)(k * dfr_step)));
+    asm volatile("" ::: "memory");
+    dfr_step = 0;
+  };
+  auto dfr_pending = [&]() { return __builtin_amdgcn_readfirstlane(dfr_step) != 0; };
+
   for (int it = 0; it < count; ++it) {
     const FwdParams p = *kernarg();  // this item's copy (shadows the prologue's reference)
     const bool group_a = opaque_uniform(wave) < C::WAVES / 2;
@@ -512,9 +536,23 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p_arg,
             f32 ? nullptr
                 : static_cast<unsigned char*>(po.out) +
                       (((int64_t)b * po.sq + row_base) * po.heads + h) * C::DPAD * 2;
-        store_rows_staged<C>(smem + wave * 32 * kStagedRowBytes<C>, lane, o,
-                             1.0f / fmaxf(tot, 1.0e-30f), f32, fdst, bdst,
-                             (int64_t)po.heads * C::DPAD * 2, po.sq - row_base);
+        if (!f32 && it + 1 < count && po.sq - row_base >= 32) {
+          // All 32 rows of the wave, and another item follows: stored after
+          // that item's first DMA.
+          unsigned char* st = smem + wave * 32 * kStagedRowBytes<C>;
+          write_staged_bf16<C>(st, opaque_lane(il), ho, o, 1.0f / fmaxf(tot, 1.0e-30f));
+          const int ln = opaque_lane(lane);
+#pragma unroll
+          for (int k = 0; k < kDefer; ++k) dfr[k] = read_staged_bf16<C>(st, ln, k);
+          const int stride = po.heads * C::DPAD * 2;
+          dfr_addr = (uint64_t)(uintptr_t)bdst +
+                     (uint64_t)(int64_t)((ln / kRowChunks) * stride) + 16u * (ln % kRowChunks);
+          dfr_step = opaque_lane(kRowsPerStore * stride);
+        } else {
+          store_rows_staged<C>(smem + wave * 32 * kStagedRowBytes<C>, lane, o,
+                               1.0f / fmaxf(tot, 1.0e-30f), f32, fdst, bdst,
+                               (int64_t)po.heads * C::DPAD * 2, po.sq - row_base);
+        }
         if (to_parts && ho == 0 && qr < po.sq)
           po.lse[(((int64_t)b * po.heads + h) * po.splits + split) * po.sq + qr] = lse_of(m, tot);
       } else if (qr < po.sq) {
@@ -636,6 +674,8 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p_arg,
       }
       issue_block(0, s0);
       if (1 < N) issue_block(1, s1);
+      const bool dfr_now = dfr_pending();
+      if (dfr_now) store_deferred();
       if (q_lds) {
         // Q has landed (its loads are older than blocks 0 and 1), in every
         // wave.
@@ -652,7 +692,18 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p_arg,
       }
 
       win1.off = block_offset<C>(p, table_b, row_bytes, key0, N, len, 64 + lane);
-      wait_block(0);
+      // The waits for blocks 0 and 1, with the deferred stores in flight
+      // behind block 1.
+      auto wait_first = [&](int j) {
+        asm volatile("" ::: "memory");
+        if (!dfr_now)
+          wait_block(j);
+        else if (j + 1 < N)
+          wait_vm<C::BATCH + kDefer>();
+        else
+          wait_vm<kDefer>();
+      };
+      wait_first(0);
       // Q has landed too (its register loads are older than block 0's; its
       // LDS reads, on the LDS path, complete here). The empty assembly makes
       // the compiler wait for them here, once, instead of
@@ -712,7 +763,7 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p_arg,
         mphase(s0, off, on);
         __syncthreads();
         sphase(0);
-        wait_block(1);
+        wait_first(1);
         __syncthreads();
         int n = 1;
         for (; n + 4 <= N; n += 4) {
@@ -740,7 +791,7 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p_arg,
         if (2 < N) issue_block(2, s2);
         __syncthreads();
         mphase(s0, off, on);
-        wait_block(1);
+        wait_first(1);
         __syncthreads();
         int n = 1;
         for (; n + 4 <= N; n += 4) {
@@ -759,6 +810,7 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p_arg,
         store_output();
       }
     } else {
+      if (dfr_pending()) store_deferred();
       store_output();
     }
   }
