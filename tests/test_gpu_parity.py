@@ -360,40 +360,46 @@ def test_prefill_layout_long_ragged_cache(page):
                          f"prefill long page={page} causal={causal} splits={kern.num_splits}")
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("dim", [64, 128])
-def test_prefill_layout_every_block_count(dim):
+def test_prefill_layout_every_block_count(dim, dtype):
     """The prefill layout's main loops run four 64-key blocks per iteration
     and the rest through a general body: requests of 0 to 11 blocks (a partial
     last block included) take every path, from no block at all through each
     remainder of the unrolled loop, against the oracle; split 2 halves them.
     Persistent grids of 1 and 3 programs run the items back to back, so that
-    every program prefetches its next item's Q rows from each of those
-    paths: bit-identical to one program per item."""
+    every program prefetches its next item's Q rows from each of those paths
+    and stores a whole-tile item's output rows after the next item's first
+    DMA (296 rows: a second tile of 40 rows, whose waves hold 32, 8 or no
+    rows): bit-identical to one program per item."""
     from fgw_amd.operators.mha.current import build_kernel
-    page, sq = 64, 256
+    page = 64
     lens = [0, 1, 64, 65, 130, 192, 256, 300, 384, 448, 512, 600, 640, 704]
     width = (max(lens) + page - 1) // page
-    case = (f"blocks_d{dim}", len(lens), sq, 1, dim, page, width)
-    q, k, v, table = O.make_inputs(case, 3, torch.bfloat16)
-    lengths = torch.tensor(lens, dtype=torch.int32)
-    k, v = O.poison_unread(k, v, table, lengths, page)
-    dev = [x.cuda() for x in (q, k, v, table, lengths)]
-    expected = O.reference(q, k, v, table, lengths, page, False)
-    for splits in (None, 2):
-        first = None
-        for persistent in (None, 1, 3):
-            kern = build_kernel(len(lens), sq, 1, dim, k.shape[0], width, page, False, "bfloat16",
-                                0, num_splits=splits, layout="prefill",
-                                persistent_programs=persistent)
-            assert kern.layout == "prefill"
-            got = kern(*dev)
-            torch.cuda.synchronize()
-            check_output(got, expected, q, lengths, False,
-                         f"prefill blocks d={dim} splits={kern.num_splits} grid={kern.compute_grid}")
-            if first is None:
-                first = got
-            else:
-                assert torch.equal(got, first), f"grid {kern.compute_grid} changed the output"
+    name = "bfloat16" if dtype == torch.bfloat16 else "float16"
+    for sq in (256, 296):
+        case = (f"blocks_d{dim}_q{sq}", len(lens), sq, 1, dim, page, width)
+        q, k, v, table = O.make_inputs(case, 3, dtype)
+        lengths = torch.tensor(lens, dtype=torch.int32)
+        k, v = O.poison_unread(k, v, table, lengths, page)
+        dev = [x.cuda() for x in (q, k, v, table, lengths)]
+        expected = O.reference(q, k, v, table, lengths, page, False)
+        for splits in (None, 2):
+            first = None
+            for persistent in (None, 1, 3):
+                kern = build_kernel(len(lens), sq, 1, dim, k.shape[0], width, page, False, name,
+                                    0, num_splits=splits, layout="prefill",
+                                    persistent_programs=persistent)
+                assert kern.layout == "prefill"
+                got = kern(*dev)
+                torch.cuda.synchronize()
+                label = (f"prefill blocks {name} d={dim} sq={sq} splits={kern.num_splits} "
+                         f"grid={kern.compute_grid}")
+                check_output(got, expected, q, lengths, False, label)
+                if first is None:
+                    first = got
+                else:
+                    assert torch.equal(got, first), f"{label}: the grid changed the output"
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
