@@ -416,24 +416,28 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p_arg,
   };
 
   // Deferred output rows. A wave's last stores of an item would sit in the
-  // vector memory counter ahead of the next item's first DMA (the counter
-  // retires loads and stores in issue order), so the waits for that item's
-  // blocks 0 and 1 would wait for them too. When another item follows, a
-  // wave with all 32 of its rows in bf16/fp16 output stages them, keeps
-  // them in dfr and stores them right after the next item's DMA of blocks 0
-  // and 1; those two waits leave them in flight, and the wait for block 2
-  // (or the last one) covers them. The address and step are held per lane,
-  // and a zero step means nothing pending.
+  // vector memory counter ahead of the next item's loads and DMA (the
+  // counter retires loads and stores in issue order), so the next item's
+  // first waits would wait for them too. When another item follows, a wave
+  // with all 32 of its rows in bf16/fp16 output stages them, keeps them in
+  // dfr and stores them once the next item's Q and block 0 have landed,
+  // ahead of the DMA of its block 2; the wait for block 1 leaves them in
+  // flight, and the wait for block 2 (or the last one) covers them. The
+  // stores name the global address space: as flat stores they would also
+  // count in the LDS counter, which every barrier waits for. The address and
+  // step are held per lane, and a zero step means nothing pending.
   constexpr int kRowChunks = C::DPAD * 2 / 16, kRowsPerStore = 64 / kRowChunks;
   constexpr int kDefer = kStagedChunks<C>;  // stores per lane
   u32x4 dfr[kDefer];
   uint64_t dfr_addr = 0;
   int dfr_step = 0;
+  typedef __attribute__((address_space(1))) u32x4 GlobalChunk;
   auto store_deferred = [&]() {
+    asm volatile("" ::: "memory");
 #pragma unroll
     for (int k = 0; k < kDefer; ++k)
       __builtin_nontemporal_store(
-          dfr[k], reinterpret_cast<u32x4*>(dfr_addr + (uint64_t)(int64_t)(k * dfr_step)));
+          dfr[k], (GlobalChunk*)(dfr_addr + (uint64_t)(int64_t)(k * dfr_step)));
     asm volatile("" ::: "memory");
     dfr_step = 0;
   };
@@ -675,7 +679,6 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p_arg,
       issue_block(0, s0);
       if (1 < N) issue_block(1, s1);
       const bool dfr_now = dfr_pending();
-      if (dfr_now) store_deferred();
       if (q_lds) {
         // Q has landed (its loads are older than blocks 0 and 1), in every
         // wave.
@@ -692,8 +695,8 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p_arg,
       }
 
       win1.off = block_offset<C>(p, table_b, row_bytes, key0, N, len, 64 + lane);
-      // The waits for blocks 0 and 1, with the deferred stores in flight
-      // behind block 1.
+      // The wait for block 1, with the deferred stores (issued after block
+      // 0's wait) in flight behind it.
       auto wait_first = [&](int j) {
         asm volatile("" ::: "memory");
         if (!dfr_now)
@@ -703,7 +706,7 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p_arg,
         else
           wait_vm<kDefer>();
       };
-      wait_first(0);
+      wait_block(0);
       // Q has landed too (its register loads are older than block 0's; its
       // LDS reads, on the LDS path, complete here). The empty assembly makes
       // the compiler wait for them here, once, instead of
@@ -711,6 +714,9 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p_arg,
       // would also wait for the DMA batch in flight.
 #pragma unroll
       for (int kk = 0; kk < C::KK; ++kk) asm volatile("" ::"v"(qf[kk]));
+      // The deferred stores go out after the compiler's wait for Q (above),
+      // which would otherwise cover them too.
+      if (dfr_now) store_deferred();
       __syncthreads();
 
       f32x16 s[C::ST];
