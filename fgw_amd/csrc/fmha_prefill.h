@@ -541,8 +541,8 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p_arg,
                 : static_cast<unsigned char*>(po.out) +
                       (((int64_t)b * po.sq + row_base) * po.heads + h) * C::DPAD * 2;
         if (!f32 && it + 1 < count && po.sq - row_base >= 32) {
-          // All 32 rows of the wave, and another item follows: stored after
-          // that item's first DMA.
+          // All 32 rows of the wave, and another item follows: stored by
+          // that item once its Q and block 0 have landed.
           unsigned char* st = smem + wave * 32 * kStagedRowBytes<C>;
           write_staged_bf16<C>(st, opaque_lane(il), ho, o, 1.0f / fmaxf(tot, 1.0e-30f));
           const int ln = opaque_lane(lane);
@@ -697,11 +697,11 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p_arg,
       win1.off = block_offset<C>(p, table_b, row_bytes, key0, N, len, 64 + lane);
       // The wait for block 1, with the deferred stores (issued after block
       // 0's wait) in flight behind it.
-      auto wait_first = [&](int j) {
+      auto wait_block1 = [&]() {
         asm volatile("" ::: "memory");
         if (!dfr_now)
-          wait_block(j);
-        else if (j + 1 < N)
+          wait_block(1);
+        else if (2 < N)
           wait_vm<C::BATCH + kDefer>();
         else
           wait_vm<kDefer>();
@@ -769,7 +769,7 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p_arg,
         mphase(s0, off, on);
         __syncthreads();
         sphase(0);
-        wait_first(1);
+        wait_block1();
         __syncthreads();
         int n = 1;
         for (; n + 4 <= N; n += 4) {
@@ -797,7 +797,7 @@ __global__ __launch_bounds__(C::THREADS) void prefill_kernel(FwdParams p_arg,
         if (2 < N) issue_block(2, s2);
         __syncthreads();
         mphase(s0, off, on);
-        wait_first(1);
+        wait_block1();
         __syncthreads();
         int n = 1;
         for (; n + 4 <= N; n += 4) {
