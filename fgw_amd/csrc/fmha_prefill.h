@@ -58,7 +58,9 @@
 // from the L2. A program with another work item to come prefetches that
 // item's Q rows into the L2 before its last blocks (after the four-block
 // main loop), so that the next item's Q loads do not queue at HBM behind
-// those of every other program.
+// those of every other program, and stores an item's output rows once the
+// next item's first block has landed (the deferred output rows below), so
+// that the next item's first waits do not wait for those stores.
 #pragma once
 #include <utility>
 
