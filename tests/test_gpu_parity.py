@@ -369,33 +369,34 @@ def test_prefill_layout_every_block_count(dim, dtype):
     remainder of the unrolled loop, against the oracle; split 2 halves them.
     Persistent grids of 1 and 3 programs run the items back to back, so that
     every program prefetches its next item's Q rows from each of those paths
-    and stores a whole-tile item's output rows after the next item's first
-    DMA (296 rows: a second tile of 40 rows, whose waves hold 32, 8 or no
-    rows): bit-identical to one program per item."""
+    and stores a whole-tile item's output rows once the next item's first
+    block has landed (296 rows: a second tile of 40 rows, whose waves hold
+    32, 8 or no rows; causal: the tiles in reverse order, with rows that see
+    no key): bit-identical to one program per item."""
     from fgw_amd.operators.mha.current import build_kernel
     page = 64
     lens = [0, 1, 64, 65, 130, 192, 256, 300, 384, 448, 512, 600, 640, 704]
     width = (max(lens) + page - 1) // page
     name = "bfloat16" if dtype == torch.bfloat16 else "float16"
-    for sq in (256, 296):
+    for sq, causal in ((256, False), (296, False), (296, True)):
         case = (f"blocks_d{dim}_q{sq}", len(lens), sq, 1, dim, page, width)
         q, k, v, table = O.make_inputs(case, 3, dtype)
         lengths = torch.tensor(lens, dtype=torch.int32)
         k, v = O.poison_unread(k, v, table, lengths, page)
         dev = [x.cuda() for x in (q, k, v, table, lengths)]
-        expected = O.reference(q, k, v, table, lengths, page, False)
+        expected = O.reference(q, k, v, table, lengths, page, causal)
         for splits in (None, 2):
             first = None
             for persistent in (None, 1, 3):
-                kern = build_kernel(len(lens), sq, 1, dim, k.shape[0], width, page, False, name,
+                kern = build_kernel(len(lens), sq, 1, dim, k.shape[0], width, page, causal, name,
                                     0, num_splits=splits, layout="prefill",
                                     persistent_programs=persistent)
                 assert kern.layout == "prefill"
                 got = kern(*dev)
                 torch.cuda.synchronize()
-                label = (f"prefill blocks {name} d={dim} sq={sq} splits={kern.num_splits} "
-                         f"grid={kern.compute_grid}")
-                check_output(got, expected, q, lengths, False, label)
+                label = (f"prefill blocks {name} d={dim} sq={sq} causal={causal} "
+                         f"splits={kern.num_splits} grid={kern.compute_grid}")
+                check_output(got, expected, q, lengths, causal, label)
                 if first is None:
                     first = got
                 else:
